@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-KV decode step at Qwen3-ASR decoder shapes.
+
+A step is one decode step of the hot path over one batch: for each of the 28
+decoder layers, reshape_and_cache of the batch's new K/V rows followed by
+paged_attention over the paged cache (the per-layer calls of
+vasr-models/src/model/thinker_text.rs:1101-1139). Default workload: c3 —
+bf16, batch 256, 16 q heads / 8 kv heads / head_dim 128, block 16, context
+lengths clip(Geom(mean 800), 16, 4096), every layer with its own pool and
+random block allocation. Inputs are synthetic (seeded) and resident in HBM
+before the timed region starts.
+
+Prints one JSON line. `value` is the whole-step HBM throughput: algorithmic
+bytes of all appends and decodes of a step divided by the step time. The
+`roofline` object covers the dominant kernel (paged_attention, main + reduce
+launch) timed with HIP events on its stream; `cpu_baseline` times the
+oracle's restatement of the reference CPU path on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "qwen3asr.rs_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
+METRIC = "paged-attn decode HBM GB/s (% of peak) + KV-append GB/s at Qwen3-ASR shapes"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="c3", choices=["c2", "c3", "c5"])
+    ap.add_argument("--layers", type=int, default=None, help="override the layer count")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU baseline budget (0 disables it)")
+    ap.add_argument("--seed", type=int, default=None)
+    return ap.parse_args()
+
+
+def build_workload(args):
+    from vpa import workloads
+
+    kw = {}
+    if args.seed is not None:
+        kw["seed"] = args.seed
+    if args.layers is not None and args.workload in ("c3", "c5"):
+        kw["num_layers"] = args.layers
+    return workloads.CONFIGS[args.workload](**kw)
+
+
+def device_tensors(w, dev):
+    import numpy as np
+    import torch
+
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w.dtype]
+    g = torch.Generator(device=dev)
+    g.manual_seed(w.seed)
+    x = 16 // w.elem_bytes
+    B, H, KVH, D, BS = w.num_seqs, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    layers = []
+    pool = None
+    for i, layer in enumerate(w.layers):
+        if pool is None or not w.shared_pool:
+            kc = torch.randn((layer.num_blocks, KVH, D // x, BS, x), generator=g, device=dev,
+                             dtype=dt)
+            vc = torch.randn((layer.num_blocks, KVH, D, BS), generator=g, device=dev, dtype=dt)
+            pool = (kc, vc)
+        kc, vc = pool
+        layers.append(dict(
+            kc=kc, vc=vc,
+            q=torch.randn((B, H, D), generator=g, device=dev, dtype=dt),
+            k=torch.randn((B, KVH, D), generator=g, device=dev, dtype=dt),
+            v=torch.randn((B, KVH, D), generator=g, device=dev, dtype=dt),
+            out=torch.empty((B, H, D), device=dev, dtype=dt),
+            bt=torch.from_numpy(layer.block_tables).to(dev),
+            slots=torch.from_numpy(layer.slot_mapping.astype(np.int64)).to(dev),
+        ))
+    ctx = torch.from_numpy(w.context_lens).to(dev)
+    return layers, ctx
+
+
+def run_step(layers, ctx, w, ws, ev=None):
+    import vpa
+
+    scale = w.head_dim ** -0.5
+    for i, L in enumerate(layers):
+        if ev is not None:
+            ev[i][0].record()
+        vpa.reshape_and_cache(L["k"], L["v"], None, None, L["kc"], L["vc"], L["slots"])
+        if ev is not None:
+            ev[i][1].record()
+        vpa.paged_attention(L["q"], None, None, L["kc"], L["vc"], L["bt"], ctx, None,
+                            w.max_context_len, scale, 1.0, None, out=L["out"], workspace=ws)
+        if ev is not None:
+            ev[i][2].record()
+
+
+def cpu_baseline(w, layers, budget_s):
+    """Time the oracle's restatement of the reference CPU decode path on a
+    bounded sample: whole layers of the same workload (all sequences), copied
+    to host memory, as many layers as fit the time budget."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    code = {"bf16": orc.BF16, "f16": orc.F16, "f32": orc.F32}[w.dtype]
+
+    def host(t):
+        import torch
+        t = t.detach().cpu().contiguous()
+        if t.dtype == torch.float32:
+            return t.numpy()
+        return t.view(torch.int16).numpy().view(np.uint16)
+
+    scale = w.head_dim ** -0.5
+    done_bytes = 0
+    elapsed = 0.0
+    layers_done = 0
+    threads = 1
+    for i, L in enumerate(layers):
+        kc, vc = host(L["kc"]), host(L["vc"])
+        q, k, v = host(L["q"]), host(L["k"]), host(L["v"])
+        meta = w.layers[i]
+        t0 = time.perf_counter()
+        _, threads = orc.cpu_baseline_decode_step(q, k, v, meta.slot_mapping, kc, vc,
+                                                  meta.block_tables, w.context_lens, scale,
+                                                  dtype=code)
+        elapsed += time.perf_counter() - t0
+        done_bytes += w.decode_bytes_per_layer() + w.append_bytes_per_layer()
+        layers_done += 1
+        if elapsed >= budget_s:
+            break
+    gbps = done_bytes / elapsed / 1e9
+    return {
+        "value": round(gbps, 3),
+        "unit": "GB/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"{layers_done} of {len(layers)} layers of {w.name} (all {w.num_seqs} "
+                   f"sequences, append + decode), {elapsed:.1f} s on {os.cpu_count()} visible "
+                   f"host CPUs"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "paged-KV path is measured per GPU, see DESIGN.md for how it would shard",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import vpa
+
+    dev = torch.device("cuda:0")
+    w = build_workload(args)
+    layers, ctx = device_tensors(w, dev)
+    ws = vpa.paged_attention_workspace(w.num_seqs, w.num_heads, w.head_dim, w.max_context_len,
+                                       dev)
+    nl = len(layers)
+
+    for _ in range(args.warmup):
+        run_step(layers, ctx, w, ws)
+    torch.cuda.synchronize()
+
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(nl)]
+          for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record()
+    for s in range(args.steps):
+        run_step(layers, ctx, w, ws, ev[s])
+    t_end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+
+    gpu_ms = t_start.elapsed_time(t_end)
+    ms_per_step = gpu_ms / args.steps
+    append_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1])
+                    for s in range(args.steps) for i in range(nl))
+    decode_ms = sum(ev[s][i][1].elapsed_time(ev[s][i][2])
+                    for s in range(args.steps) for i in range(nl))
+    launches = args.steps * nl
+    dec_bytes = w.decode_bytes_per_layer()
+    app_bytes = w.append_bytes_per_layer()
+    step_bytes = nl * (dec_bytes + app_bytes)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    dec_launch_ms = decode_ms / launches
+    app_launch_ms = append_ms / launches
+    dec_gbps = dec_bytes / (dec_launch_ms * 1e-3) / 1e9
+    app_gbps = app_bytes / (app_launch_ms * 1e-3) / 1e9
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"paged_decode_{w.name}_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(w, layers, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": "synthetic (seeded)",
+        "config": {
+            "workload": w.name,
+            "num_seqs": w.num_seqs,
+            "layers": nl,
+            "q_heads": w.num_heads,
+            "kv_heads": w.num_kv_heads,
+            "head_dim": w.head_dim,
+            "block_size": w.block_size,
+            "context_tokens": int(w.context_lens.sum()),
+            "max_context_len": w.max_context_len,
+            "seed": w.seed,
+        },
+        "decode_gbps": round(dec_gbps, 2),
+        "decode_frac_of_peak": round(dec_gbps / HBM_PEAK_GBPS, 4),
+        "append_gbps": round(app_gbps, 2),
+        "append_us_per_launch": round(app_launch_ms * 1e3, 2),
+        "wall_s_timed_region": round(wall, 4),
+        "roofline": {
+            "kernel": "paged_attention (decode main + split-K reduce)",
+            "bound": "hbm",
+            "achieved": round(dec_gbps, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": dec_bytes,
+            "us_per_launch": round(dec_launch_ms * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

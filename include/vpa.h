@@ -1,0 +1,170 @@
+/*
+ * vpa.h — C ABI of the MI355X (gfx950) paged-KV hot path for the Qwen3-ASR
+ * text decoder.
+ *
+ * The entry points replace the three Candle ops that vASR imports from the
+ * external crate `mistralrs-paged-attn` (re-exported at
+ * vasr-paged-attn/src/lib.rs:20-21) plus the paged chunked-prefill attention,
+ * keeping the reference's cache layouts and metadata semantics:
+ *
+ *   key_cache   [num_blocks, num_kv_heads, head_dim / x, block_size, x]
+ *   value_cache [num_blocks, num_kv_heads, head_dim, block_size]
+ *   x = 16 / sizeof(cache element)          (vasr-paged-attn/src/paged_kv_cache.rs:263-294)
+ *
+ *   slot_mapping  int64  [num_tokens]; slot = block_id * block_size + offset,
+ *                 negative = padding, skipped            (paged_kv_cache.rs:7, 74-103)
+ *   block_tables  uint32 [num_seqs, block_table_stride]  (paged_kv_cache.rs:954-964)
+ *   context_lens  uint32 [num_seqs]                      (paged_kv_cache.rs:985-1017)
+ *   cu_seqlens    uint32 [num_seqs + 1]                  (paged_kv_cache.rs:58-72)
+ *
+ * Conventions of this ABI:
+ *   - All pointers to tensors are device pointers; sizes, strides and scalar
+ *     parameters are host values. Strides are in elements.
+ *   - Every argument check happens on the host before any launch. A failed
+ *     check returns a non-zero status and sets a thread-local message read by
+ *     vpa_last_error(). Nothing is launched in that case.
+ *   - No entry point allocates device memory, synchronises, or reads device
+ *     memory from the host, so every launch may be recorded into a HIP graph.
+ *     Scratch memory comes from the caller (see
+ *     vpa_paged_attention_workspace_size).
+ *   - `stream` is a hipStream_t (NULL = the null stream).
+ *   - The library is reentrant; its only global state is the thread-local
+ *     error message.
+ */
+#ifndef VPA_H_
+#define VPA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define VPA_OK 0
+#define VPA_ERR_INVALID_ARGUMENT 1 /* shape, stride, null pointer, mismatch   */
+#define VPA_ERR_UNSUPPORTED 2      /* dtype / head_dim / block_size / option  */
+#define VPA_ERR_WORKSPACE 3        /* caller workspace too small             */
+#define VPA_ERR_HIP 4              /* the HIP runtime reported an error       */
+#define VPA_ERR_CAPACITY 5         /* KV pool exhausted (block manager)       */
+#define VPA_ERR_NOT_FOUND 6        /* unknown request id (block manager)      */
+
+/* ---- element types --------------------------------------------------- */
+#define VPA_DTYPE_F32 0
+#define VPA_DTYPE_F16 1
+#define VPA_DTYPE_BF16 2
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* vpa_last_error(void);
+
+/* Library version string. */
+const char* vpa_version(void);
+
+/*
+ * Shapes of one layer's key and value cache for a pool of `num_blocks`
+ * blocks. Restates PagedKvCache::new_inner (paged_kv_cache.rs:229-314):
+ * x = 16 / dtype_bytes, head_dim must be a multiple of x, every size
+ * non-zero. Fills key_shape[5] and value_shape[4].
+ */
+int vpa_cache_layout(int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     int64_t num_blocks, int32_t cache_dtype, int64_t* key_shape,
+                     int64_t* value_shape);
+
+/*
+ * reshape_and_cache — write new K/V rows into the paged cache.
+ * Replaces mistralrs_paged_attn::reshape_and_cache(key, value, k_scale,
+ * v_scale, key_cache, value_cache, slot_mapping) called at
+ * vasr-models/src/model/thinker_text.rs:1101-1109 (decode) and :1324-1332
+ * (packed prefill).
+ *
+ * key/value: [num_tokens, num_kv_heads, head_dim], head stride head_dim, token
+ * stride key_token_stride / value_token_stride (>= num_kv_heads*head_dim).
+ * For token t with s = slot_mapping[t] >= 0: blk = s / block_size,
+ * off = s % block_size,
+ *   key_cache  [blk, j, d / x, off, d % x] = key  [t, j, d]
+ *   value_cache[blk, j, d, off]            = value[t, j, d]
+ * Slots < 0 (PAD_SLOT_ID) and slots >= num_blocks*block_size are skipped.
+ * The copy is bit-exact. k_scale / v_scale may be NULL; they are ignored
+ * because cache_dtype must equal dtype (no fp8 cache in this build).
+ * num_tokens == 0 is a no-op.
+ *
+ * Cache strides: cache_block_stride / cache_head_stride are the element
+ * strides of the first two dims of both caches (a (block, head) tile is
+ * head_dim*block_size contiguous elements in both).
+ */
+int vpa_reshape_and_cache(const void* key, const void* value, int64_t key_token_stride,
+                          int64_t value_token_stride, const float* k_scale,
+                          const float* v_scale, void* key_cache, void* value_cache,
+                          const int64_t* slot_mapping, int64_t num_tokens,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int64_t num_blocks, int64_t cache_block_stride,
+                          int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
+                          void* stream);
+
+/*
+ * Bytes of caller workspace vpa_paged_attention needs for split-K partials
+ * (partial outputs, maxima and sums) at this shape. Depends only on the
+ * arguments; 0 is never returned for valid sizes.
+ */
+size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
+                                          int32_t head_dim, int32_t max_context_len);
+
+/*
+ * paged_attention — single-token decode over the paged cache.
+ * Replaces mistralrs_paged_attn::paged_attention(q, k_scale, v_scale,
+ * key_cache, value_cache, block_tables, context_lens, alibi_slopes,
+ * max_context_len, softmax_scale, softcapping, sinks) called at
+ * vasr-models/src/model/thinker_text.rs:1126-1139.
+ *
+ * query/out: [num_seqs, num_heads, head_dim] packed, same dtype. For sequence
+ * s, q head h, kv head j = h / (num_heads / num_kv_heads)
+ * (attention.rs:12-21) and L = min(context_lens[s], max_context_len):
+ *   p = softmax_t(softmax_scale * q[s,h] . K[s,j,t]),  t < L
+ *   out[s,h] = sum_t p_t V[s,j,t] / (sum_t p_t + 1e-6)  (unnormalised p)
+ * where token t lives in block block_tables[s, t / block_size]. Entries
+ * >= num_blocks are treated as absent (their tokens are skipped). L == 0
+ * gives zeros. max_context_len bounds the split-K grid only (a value frozen
+ * at graph capture is fine as long as it is >= every context_len).
+ * alibi_slopes and sinks must be NULL and softcapping must be 1.0 (the only
+ * values vASR passes); anything else returns VPA_ERR_UNSUPPORTED.
+ * workspace must hold vpa_paged_attention_workspace_size(...) bytes and be
+ * 256-byte aligned; it may be NULL when that size is 0.
+ */
+int vpa_paged_attention(void* out, const void* query, const float* k_scale,
+                        const float* v_scale, const void* key_cache, const void* value_cache,
+                        const uint32_t* block_tables, int32_t block_table_stride,
+                        const uint32_t* context_lens, const float* alibi_slopes,
+                        int32_t max_context_len, float softmax_scale, float softcapping,
+                        const float* sinks, int32_t num_seqs, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int64_t num_blocks, int64_t cache_block_stride,
+                        int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * gather_kv_cache — copy each sequence's first kv_len tokens out of the paged
+ * cache into packed rows.
+ * Replaces mistralrs_paged_attn::gather_kv_cache(key_cache, value_cache,
+ * k_scale, v_scale, block_tables, cu_seqlens_kv, out_dtype) called at
+ * vasr-models/src/model/thinker_text.rs:190-198 and :1344-1352.
+ *
+ * out_key/out_value: [total_tokens, num_kv_heads, head_dim] packed in
+ * out_dtype; row cu_seqlens_kv[s] + t holds token t of sequence s.
+ * total_tokens must equal cu_seqlens_kv[num_seqs] (the host knows it from
+ * kv_lens). Block ids >= num_blocks produce zero rows.
+ */
+int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
+                        const void* value_cache, const float* k_scale, const float* v_scale,
+                        const uint32_t* block_tables, int32_t block_table_stride,
+                        const uint32_t* cu_seqlens_kv, int32_t num_seqs, int64_t total_tokens,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int64_t num_blocks, int64_t cache_block_stride,
+                        int64_t cache_head_stride, int32_t cache_dtype, int32_t out_dtype,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VPA_H_ */

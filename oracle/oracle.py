@@ -1,0 +1,198 @@
+"""TEST INFRASTRUCTURE ONLY — numpy/ctypes face of the CPU oracle.
+
+Wraps ``oracle/libvpa_oracle.so`` (built from ``oracle/vpa_oracle.c``) for
+numpy arrays. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this module; the product path never does.
+
+The restated reference semantics and their file:line sources are listed in
+the header of ``vpa_oracle.c``. In short: the paged cache layout of
+``vasr-paged-attn/src/paged_kv_cache.rs:263-294``, slot mapping with
+``PAD_SLOT_ID`` skip (``paged_kv_cache.rs:7, 74-103, 697-700``), GQA
+``repeat_kv`` (``vasr-models/src/model/attention.rs:12-21``), eager softmax
+attention (``attention.rs:243-286``), cached causal mask
+(``attention.rs:78-149``) and the ``+1e-6`` softmax denominator of the paged
+sibling kernel (``prefill_paged_attn.metal:1300``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+F32, F16, BF16 = 0, 1, 2
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libvpa_oracle.so")
+_lib = None
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_dbl = ctypes.c_double
+_flt = ctypes.c_float
+
+
+def build() -> None:
+    """Compile libvpa_oracle.so with the Makefile beside this file."""
+    subprocess.run(["make", "-B", "-C", _HERE], check=True, capture_output=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.oracle_reshape_and_cache.argtypes = [_i32, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i32,
+                                               _i32, _i32, _i64, _i64, _i64]
+        L.oracle_reshape_and_cache.restype = None
+        L.oracle_gather_kv_cache.argtypes = [_i32, _p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32,
+                                             _i32, _i64, _i64, _i64]
+        L.oracle_gather_kv_cache.restype = None
+        L.oracle_paged_attention_f64.argtypes = [_i32, _p, _p, _p, _p, _p, _i32, _p, _i32, _dbl,
+                                                 _i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64]
+        L.oracle_paged_attention_f64.restype = None
+        L.oracle_prefill_attention_f64.argtypes = [_i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i32,
+                                                   _i32, _dbl, _i32, _i32, _i32, _i32, _i64,
+                                                   _i64, _i64]
+        L.oracle_prefill_attention_f64.restype = None
+        L.cpu_baseline_decode_step.argtypes = [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _p,
+                                               _flt, _i32, _i32, _i32, _i32, _i32, _i64, _i64,
+                                               _i64]
+        L.cpu_baseline_decode_step.restype = _i32
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def dtype_code(a: np.ndarray, code: int | None = None) -> int:
+    """16-bit data travels as uint16 words; the caller names bf16 vs f16."""
+    if code is not None:
+        return code
+    if a.dtype == np.float32:
+        return F32
+    raise ValueError("16-bit arrays need an explicit dtype code (F16 or BF16)")
+
+
+def _cache_geom(key_cache: np.ndarray):
+    nb, kvh, dx, bs, x = key_cache.shape
+    return nb, kvh, dx * x, bs, kvh * dx * bs * x, dx * bs * x
+
+
+def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, dtype=None):
+    """In-place append of key/value rows [T, KVH, D] into the caches."""
+    code = dtype_code(key, dtype)
+    nb, kvh, d, bs, bstride, hstride = _cache_geom(key_cache)
+    t = key.shape[0]
+    slot_mapping = np.ascontiguousarray(slot_mapping, dtype=np.int64)
+    lib().oracle_reshape_and_cache(code, _ptr(key), _ptr(value), kvh * d, kvh * d,
+                                   _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping), t,
+                                   kvh, d, bs, nb, bstride, hstride)
+
+
+def gather_kv_cache(key_cache, value_cache, block_tables, cu_seqlens, dtype=None):
+    code = dtype_code(key_cache, dtype)
+    nb, kvh, d, bs, bstride, hstride = _cache_geom(key_cache)
+    block_tables = np.ascontiguousarray(block_tables, dtype=np.uint32)
+    cu_seqlens = np.ascontiguousarray(cu_seqlens, dtype=np.uint32)
+    rows = int(cu_seqlens[-1])
+    ok = np.zeros((rows, kvh, d), dtype=key_cache.dtype)
+    ov = np.zeros((rows, kvh, d), dtype=key_cache.dtype)
+    lib().oracle_gather_kv_cache(code, _ptr(ok), _ptr(ov), _ptr(key_cache), _ptr(value_cache),
+                                 _ptr(block_tables), block_tables.shape[1], _ptr(cu_seqlens),
+                                 block_tables.shape[0], kvh, d, bs, nb, bstride, hstride)
+    return ok, ov
+
+
+def paged_attention(q, key_cache, value_cache, block_tables, context_lens, max_context_len,
+                    scale, dtype=None) -> np.ndarray:
+    """Decode attention, float64 result [B, H, D]."""
+    code = dtype_code(q, dtype)
+    nb, kvh, d, bs, bstride, hstride = _cache_geom(key_cache)
+    b, h, _ = q.shape
+    block_tables = np.ascontiguousarray(block_tables, dtype=np.uint32)
+    context_lens = np.ascontiguousarray(context_lens, dtype=np.uint32)
+    out = np.zeros((b, h, d), dtype=np.float64)
+    lib().oracle_paged_attention_f64(code, _ptr(out), _ptr(q), _ptr(key_cache), _ptr(value_cache),
+                                     _ptr(block_tables), block_tables.shape[1], _ptr(context_lens),
+                                     int(max_context_len), float(scale), b, h, kvh, d, bs, nb,
+                                     bstride, hstride)
+    return out
+
+
+def prefill_attention(q, key_cache, value_cache, block_tables, context_lens, cu_seqlens_q, scale,
+                      causal=True, dtype=None) -> np.ndarray:
+    """Chunked prefill attention over the paged cache, float64 [total_q, H, D]."""
+    code = dtype_code(q, dtype)
+    nb, kvh, d, bs, bstride, hstride = _cache_geom(key_cache)
+    tq, h, _ = q.shape
+    block_tables = np.ascontiguousarray(block_tables, dtype=np.uint32)
+    context_lens = np.ascontiguousarray(context_lens, dtype=np.uint32)
+    cu_seqlens_q = np.ascontiguousarray(cu_seqlens_q, dtype=np.uint32)
+    out = np.zeros((tq, h, d), dtype=np.float64)
+    lib().oracle_prefill_attention_f64(code, _ptr(out), _ptr(q), _ptr(key_cache),
+                                       _ptr(value_cache), _ptr(block_tables), block_tables.shape[1],
+                                       _ptr(context_lens), _ptr(cu_seqlens_q),
+                                       block_tables.shape[0], int(bool(causal)), float(scale), h,
+                                       kvh, d, bs, nb, bstride, hstride)
+    return out
+
+
+def cpu_baseline_decode_step(q, new_key, new_value, slot_mapping, key_cache, value_cache,
+                             block_tables, context_lens, scale, dtype=None):
+    """The reference's CPU decode path (append + gather + eager attention) in f32.
+
+    Returns (out [B, H, D] float32, threads used)."""
+    code = dtype_code(q, dtype)
+    nb, kvh, d, bs, bstride, hstride = _cache_geom(key_cache)
+    b, h, _ = q.shape
+    out = np.zeros((b, h, d), dtype=np.float32)
+    slot_mapping = np.ascontiguousarray(slot_mapping, dtype=np.int64)
+    block_tables = np.ascontiguousarray(block_tables, dtype=np.uint32)
+    context_lens = np.ascontiguousarray(context_lens, dtype=np.uint32)
+    threads = lib().cpu_baseline_decode_step(code, _ptr(out), _ptr(q), _ptr(new_key),
+                                             _ptr(new_value), _ptr(slot_mapping), _ptr(key_cache),
+                                             _ptr(value_cache), _ptr(block_tables),
+                                             block_tables.shape[1], _ptr(context_lens),
+                                             float(scale), b, h, kvh, d, bs, nb, bstride, hstride)
+    return out, threads
+
+
+# ---- element conversions used by tests to build inputs -------------------
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bf16 words (uint16)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return rounded.astype(np.uint16)
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(h, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def to_f32(a: np.ndarray, code: int) -> np.ndarray:
+    if code == F32:
+        return np.asarray(a, dtype=np.float32)
+    return bf16_bits_to_f32(a) if code == BF16 else f16_bits_to_f32(a)
+
+
+def from_f32(a: np.ndarray, code: int) -> np.ndarray:
+    if code == F32:
+        return np.ascontiguousarray(a, dtype=np.float32)
+    return f32_to_bf16_bits(a) if code == BF16 else f32_to_f16_bits(a)

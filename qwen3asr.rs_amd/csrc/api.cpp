@@ -1,0 +1,306 @@
+// C-ABI entry points of libvpa: host-side argument checks, then kernel
+// launches. Every check runs before anything is launched; a failure returns a
+// status code and leaves a message for vpa_last_error().
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "vpa_internal.h"
+
+namespace vpa {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error.assign(buf);
+  return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+namespace {
+
+int dtype_bytes(int32_t dtype) {
+  switch (dtype) {
+    case VPA_DTYPE_F32:
+      return 4;
+    case VPA_DTYPE_F16:
+    case VPA_DTYPE_BF16:
+      return 2;
+    default:
+      return 0;
+  }
+}
+
+const char* dtype_name(int32_t dtype) {
+  switch (dtype) {
+    case VPA_DTYPE_F32:
+      return "f32";
+    case VPA_DTYPE_F16:
+      return "f16";
+    case VPA_DTYPE_BF16:
+      return "bf16";
+    default:
+      return "unknown";
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks shared by every op that reads or writes the paged cache.
+int check_cache(const char* op, int32_t cache_dtype, int32_t num_kv_heads, int32_t head_dim,
+                int32_t block_size, int64_t num_blocks, int64_t block_stride,
+                int64_t head_stride, const void* key_cache, const void* value_cache) {
+  const int eb = dtype_bytes(cache_dtype);
+  if (eb == 0) return fail(VPA_ERR_UNSUPPORTED, "%s: unsupported cache dtype %d", op, cache_dtype);
+  if (num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks <= 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: sizes must be positive: num_kv_heads=%d head_dim=%d block_size=%d "
+                "num_blocks=%lld",
+                op, num_kv_heads, head_dim, block_size, (long long)num_blocks);
+  const int x = 16 / eb;
+  if (head_dim % x != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: head_dim must be divisible by key cache pack size: head_dim=%d pack=%d", op,
+                head_dim, x);
+  if (!cache_kernels_supported(cache_dtype, head_dim, block_size))
+    return fail(VPA_ERR_UNSUPPORTED,
+                "%s: no kernel for dtype=%s head_dim=%d block_size=%d (head_dim in "
+                "{64,128,256}, block_size in {8,16,32})",
+                op, dtype_name(cache_dtype), head_dim, block_size);
+  const int64_t tile = (int64_t)head_dim * block_size;
+  if (head_stride < tile || block_stride < head_stride * num_kv_heads)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: cache strides overlap tiles: block_stride=%lld head_stride=%lld tile=%lld "
+                "num_kv_heads=%d",
+                op, (long long)block_stride, (long long)head_stride, (long long)tile,
+                num_kv_heads);
+  if ((head_stride * eb) % 16 != 0 || (block_stride * eb) % 16 != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: cache strides must be multiples of 16 bytes: block_stride=%lld "
+                "head_stride=%lld",
+                op, (long long)block_stride, (long long)head_stride);
+  if (key_cache == nullptr || value_cache == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: key_cache and value_cache must be non-null", op);
+  if (!aligned16(key_cache) || !aligned16(value_cache))
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: caches must be 16-byte aligned", op);
+  return VPA_OK;
+}
+
+int hip_status(const char* op, hipError_t e) {
+  if (e == hipSuccess) return VPA_OK;
+  return fail(VPA_ERR_HIP, "%s: HIP launch failed: %s", op, hipGetErrorString(e));
+}
+
+}  // namespace
+}  // namespace vpa
+
+using namespace vpa;
+
+extern "C" {
+
+const char* vpa_last_error(void) { return g_last_error.c_str(); }
+
+const char* vpa_version(void) { return "vpa 0.1.0 (gfx950)"; }
+
+int vpa_cache_layout(int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     int64_t num_blocks, int32_t cache_dtype, int64_t* key_shape,
+                     int64_t* value_shape) {
+  clear_error();
+  if (key_shape == nullptr || value_shape == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "vpa_cache_layout: shape outputs must be non-null");
+  if (num_kv_heads <= 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "paged kv cache requires at least one kv head");
+  if (head_dim <= 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "paged kv cache requires non-zero head_dim");
+  if (block_size <= 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "paged kv cache requires non-zero block_size");
+  if (num_blocks <= 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "paged kv cache requires non-zero num_blocks");
+  const int eb = dtype_bytes(cache_dtype);
+  if (eb == 0)
+    return fail(VPA_ERR_UNSUPPORTED, "unsupported paged kv cache dtype: %d", cache_dtype);
+  const int x = 16 / eb;
+  if (head_dim % x != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "head_dim must be divisible by key cache pack size: head_dim=%d pack=%d",
+                head_dim, x);
+  key_shape[0] = num_blocks;
+  key_shape[1] = num_kv_heads;
+  key_shape[2] = head_dim / x;
+  key_shape[3] = block_size;
+  key_shape[4] = x;
+  value_shape[0] = num_blocks;
+  value_shape[1] = num_kv_heads;
+  value_shape[2] = head_dim;
+  value_shape[3] = block_size;
+  return VPA_OK;
+}
+
+int vpa_reshape_and_cache(const void* key, const void* value, int64_t key_token_stride,
+                          int64_t value_token_stride, const float* k_scale,
+                          const float* v_scale, void* key_cache, void* value_cache,
+                          const int64_t* slot_mapping, int64_t num_tokens,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int64_t num_blocks, int64_t cache_block_stride,
+                          int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
+                          void* stream) {
+  (void)k_scale;
+  (void)v_scale;
+  clear_error();
+  const char* op = "reshape_and_cache";
+  if (num_tokens < 0) return fail(VPA_ERR_INVALID_ARGUMENT, "%s: num_tokens < 0", op);
+  if (dtype != cache_dtype)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from input dtype %s", op,
+                dtype_name(cache_dtype), dtype_name(dtype));
+  int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
+                       cache_block_stride, cache_head_stride, key_cache, value_cache);
+  if (rc != VPA_OK) return rc;
+  if (num_tokens == 0) return VPA_OK;
+  if (key == nullptr || value == nullptr || slot_mapping == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: key, value and slot_mapping must be non-null", op);
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  if (key_token_stride < row || value_token_stride < row)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: token stride (key=%lld value=%lld) smaller than num_kv_heads*head_dim=%lld",
+                op, (long long)key_token_stride, (long long)value_token_stride, (long long)row);
+  const int eb = dtype_bytes(dtype);
+  if (!aligned16(key) || !aligned16(value) || (key_token_stride * eb) % 16 != 0 ||
+      (value_token_stride * eb) % 16 != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: key/value rows must be 16-byte aligned", op);
+  if ((num_tokens + block_size - 1) / block_size > 0x7fffffffLL)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: too many tokens: %lld", op, (long long)num_tokens);
+  CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
+              cache_head_stride};
+  return hip_status(op, launch_reshape_and_cache(dtype, key, value, key_token_stride,
+                                                 value_token_stride, key_cache, value_cache,
+                                                 slot_mapping, num_tokens, g,
+                                                 static_cast<hipStream_t>(stream)));
+}
+
+size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
+                                          int32_t head_dim, int32_t max_context_len) {
+  return decode_workspace_bytes(num_seqs, num_heads, head_dim, max_context_len);
+}
+
+int vpa_paged_attention(void* out, const void* query, const float* k_scale,
+                        const float* v_scale, const void* key_cache, const void* value_cache,
+                        const uint32_t* block_tables, int32_t block_table_stride,
+                        const uint32_t* context_lens, const float* alibi_slopes,
+                        int32_t max_context_len, float softmax_scale, float softcapping,
+                        const float* sinks, int32_t num_seqs, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int64_t num_blocks, int64_t cache_block_stride,
+                        int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  (void)k_scale;
+  (void)v_scale;
+  clear_error();
+  const char* op = "paged_attention";
+  if (alibi_slopes != nullptr)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: alibi_slopes are not supported", op);
+  if (sinks != nullptr) return fail(VPA_ERR_UNSUPPORTED, "%s: sinks are not supported", op);
+  if (softcapping != 1.0f)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: softcapping must be 1.0 (off), got %g", op,
+                (double)softcapping);
+  if (dtype != cache_dtype)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from query dtype %s", op,
+                dtype_name(cache_dtype), dtype_name(dtype));
+  int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
+                       cache_block_stride, cache_head_stride, key_cache, value_cache);
+  if (rc != VPA_OK) return rc;
+  if (num_seqs < 0 || num_heads <= 0 || max_context_len < 0 || block_table_stride < 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: bad sizes num_seqs=%d num_heads=%d max_context_len=%d "
+                "block_table_stride=%d",
+                op, num_seqs, num_heads, max_context_len, block_table_stride);
+  if (num_heads % num_kv_heads != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: num_heads=%d not a multiple of num_kv_heads=%d",
+                op, num_heads, num_kv_heads);
+  const int group = num_heads / num_kv_heads;
+  if (!decode_supported(dtype, head_dim, block_size, group))
+    return fail(VPA_ERR_UNSUPPORTED,
+                "%s: no kernel for %d query heads per kv head (supported: 1, 2, 4)", op, group);
+  if (max_context_len > kDecodeMaxPartitions * kDecodePartitionTokens)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: max_context_len=%d exceeds %d", op, max_context_len,
+                kDecodeMaxPartitions * kDecodePartitionTokens);
+  if (num_seqs == 0) return VPA_OK;
+  if (num_seqs > 65535)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: num_seqs=%d exceeds 65535", op, num_seqs);
+  if (out == nullptr || query == nullptr || block_tables == nullptr || context_lens == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: out, query, block_tables and context_lens must be non-null", op);
+  if (!aligned16(out) || !aligned16(query))
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: out and query must be 16-byte aligned", op);
+  if (max_context_len > 0 && (int64_t)block_table_stride * block_size < max_context_len)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: block_table_stride=%d too small for max_context_len=%d (block_size=%d)", op,
+                block_table_stride, max_context_len, block_size);
+  const size_t need = decode_workspace_bytes(num_seqs, num_heads, head_dim, max_context_len);
+  if (need > 0) {
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(VPA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", op, need,
+                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(VPA_ERR_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned", op);
+  }
+  CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
+              cache_head_stride};
+  DecodeWorkspace ws =
+      carve_decode_workspace(workspace, num_seqs, num_heads, head_dim, max_context_len);
+  return hip_status(op, launch_paged_decode(dtype, out, query, key_cache, value_cache,
+                                            block_tables, block_table_stride, context_lens,
+                                            max_context_len, softmax_scale, num_seqs, num_heads,
+                                            g, ws, static_cast<hipStream_t>(stream)));
+}
+
+int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
+                        const void* value_cache, const float* k_scale, const float* v_scale,
+                        const uint32_t* block_tables, int32_t block_table_stride,
+                        const uint32_t* cu_seqlens_kv, int32_t num_seqs, int64_t total_tokens,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int64_t num_blocks, int64_t cache_block_stride,
+                        int64_t cache_head_stride, int32_t cache_dtype, int32_t out_dtype,
+                        void* stream) {
+  (void)k_scale;
+  (void)v_scale;
+  clear_error();
+  const char* op = "gather_kv_cache";
+  if (out_dtype != cache_dtype)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: out dtype %s differs from cache dtype %s", op,
+                dtype_name(out_dtype), dtype_name(cache_dtype));
+  int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
+                       cache_block_stride, cache_head_stride, key_cache, value_cache);
+  if (rc != VPA_OK) return rc;
+  if (num_seqs < 0 || total_tokens < 0 || block_table_stride < 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: bad sizes num_seqs=%d total_tokens=%lld block_table_stride=%d", op, num_seqs,
+                (long long)total_tokens, block_table_stride);
+  if (num_seqs == 0 || total_tokens == 0 || block_table_stride == 0) return VPA_OK;
+  if (num_seqs > 65535)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: num_seqs=%d exceeds 65535", op, num_seqs);
+  if (out_key == nullptr || out_value == nullptr || block_tables == nullptr ||
+      cu_seqlens_kv == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: outputs, block_tables and cu_seqlens_kv must be non-null", op);
+  if (!aligned16(out_key) || !aligned16(out_value))
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: outputs must be 16-byte aligned", op);
+  CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
+              cache_head_stride};
+  return hip_status(op, launch_gather_kv_cache(cache_dtype, out_key, out_value, key_cache,
+                                               value_cache, block_tables, block_table_stride,
+                                               cu_seqlens_kv, num_seqs, g,
+                                               static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

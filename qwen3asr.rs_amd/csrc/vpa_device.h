@@ -1,0 +1,147 @@
+// Device-side helpers shared by the gfx950 kernels: element types, 16-byte
+// vector access, conversions and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vpa {
+
+// Storage types. bf16 and f16 are handled as raw 16-bit words so that copies
+// stay bit-exact; arithmetic converts explicitly.
+struct bf16_t {
+  uint16_t x;
+};
+struct f16_t {
+  uint16_t x;
+};
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2_t;
+
+template <typename T>
+struct ElemTraits;
+template <>
+struct ElemTraits<float> {
+  static constexpr int kBytes = 4;
+};
+template <>
+struct ElemTraits<bf16_t> {
+  static constexpr int kBytes = 2;
+};
+template <>
+struct ElemTraits<f16_t> {
+  static constexpr int kBytes = 2;
+};
+
+// Elements per 16-byte vector: the key-cache pack factor x of the layout.
+template <typename T>
+constexpr int pack_x() {
+  return 16 / ElemTraits<T>::kBytes;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+// Round-to-nearest-even f32 -> bf16 (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return (float)v;
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 v = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, v);
+}
+
+template <typename T>
+__device__ __forceinline__ void store_from_f32(T* p, float v);
+template <>
+__device__ __forceinline__ void store_from_f32<float>(float* p, float v) {
+  *p = v;
+}
+template <>
+__device__ __forceinline__ void store_from_f32<bf16_t>(bf16_t* p, float v) {
+  p->x = f32_to_bf16_bits(v);
+}
+template <>
+__device__ __forceinline__ void store_from_f32<f16_t>(f16_t* p, float v) {
+  p->x = f32_to_f16_bits(v);
+}
+
+// Two adjacent f32 values packed into one 32-bit word of two 16-bit elements
+// (low half = first element).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) {
+  return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+}
+
+// acc + a.lo*b.lo + a.hi*b.hi for two packed 16-bit pairs (v_dot2 on gfx950).
+template <typename T>
+__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float acc);
+template <>
+__device__ __forceinline__ float dot2_acc<bf16_t>(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+template <>
+__device__ __forceinline__ float dot2_acc<f16_t>(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
+                                acc, false);
+}
+
+// Dot product of two 16-byte vectors of T, accumulated in f32.
+template <typename T>
+__device__ __forceinline__ float dot16(const uint4& a, const uint4& b, float acc) {
+  acc = dot2_acc<T>(a.x, b.x, acc);
+  acc = dot2_acc<T>(a.y, b.y, acc);
+  acc = dot2_acc<T>(a.z, b.z, acc);
+  acc = dot2_acc<T>(a.w, b.w, acc);
+  return acc;
+}
+template <>
+__device__ __forceinline__ float dot16<float>(const uint4& a, const uint4& b, float acc) {
+  acc = fmaf(__uint_as_float(a.x), __uint_as_float(b.x), acc);
+  acc = fmaf(__uint_as_float(a.y), __uint_as_float(b.y), acc);
+  acc = fmaf(__uint_as_float(a.z), __uint_as_float(b.z), acc);
+  acc = fmaf(__uint_as_float(a.w), __uint_as_float(b.w), acc);
+  return acc;
+}
+
+// Wave64 butterfly reductions; every lane ends with the result.
+template <int kFirst, int kLast>
+__device__ __forceinline__ float wave_max_range(float v) {
+#pragma unroll
+  for (int m = kFirst; m <= kLast; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+template <int kFirst, int kLast>
+__device__ __forceinline__ float wave_sum_range(float v) {
+#pragma unroll
+  for (int m = kFirst; m <= kLast; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Wait until this wave's LDS operations have completed (lgkmcnt(0) only, so
+// outstanding global loads stay in flight), and keep the compiler from
+// moving LDS accesses across the wait.
+__device__ __forceinline__ void lds_wave_sync() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+}
+
+}  // namespace vpa

@@ -1,0 +1,70 @@
+// Host-side internals shared by the C-ABI layer and the kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/vpa.h"
+
+namespace vpa {
+
+// Thread-local error message; returns `code` for tail calls.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Geometry of one layer's paged cache (both K and V tiles are
+// head_dim*block_size contiguous elements per (block, head)).
+struct CacheGeom {
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t block_size;
+  int64_t num_blocks;
+  int64_t block_stride;  // elements
+  int64_t head_stride;   // elements
+};
+
+// Decode split-K partition length in tokens (a multiple of every supported
+// block size).
+constexpr int kDecodePartitionTokens = 256;
+// Upper bound on split-K partitions per sequence handled by the reduce kernel.
+constexpr int kDecodeMaxPartitions = 2048;
+
+struct DecodeWorkspace {
+  float* part_out;  // [num_seqs, num_heads, max_parts, head_dim]
+  float* part_max;  // [num_seqs, num_heads, max_parts]
+  float* part_sum;  // [num_seqs, num_heads, max_parts]
+  int max_parts;
+};
+
+size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len);
+DecodeWorkspace carve_decode_workspace(void* base, int num_seqs, int num_heads, int head_dim,
+                                       int max_context_len);
+
+// Launchers return hipSuccess or the launch error. Arguments are validated by
+// the caller.
+hipError_t launch_reshape_and_cache(int dtype, const void* key, const void* value,
+                                    int64_t key_token_stride, int64_t value_token_stride,
+                                    void* key_cache, void* value_cache,
+                                    const int64_t* slot_mapping, int64_t num_tokens,
+                                    const CacheGeom& g, hipStream_t stream);
+
+hipError_t launch_gather_kv_cache(int dtype, void* out_key, void* out_value,
+                                  const void* key_cache, const void* value_cache,
+                                  const uint32_t* block_tables, int32_t block_table_stride,
+                                  const uint32_t* cu_seqlens, int32_t num_seqs,
+                                  const CacheGeom& g, hipStream_t stream);
+
+hipError_t launch_paged_decode(int dtype, void* out, const void* query, const void* key_cache,
+                               const void* value_cache, const uint32_t* block_tables,
+                               int32_t block_table_stride, const uint32_t* context_lens,
+                               int32_t max_context_len, float scale, int32_t num_seqs,
+                               int32_t num_heads, const CacheGeom& g, const DecodeWorkspace& ws,
+                               hipStream_t stream);
+
+// True when a decode kernel is compiled for this (dtype, head_dim, block_size,
+// query heads per kv head) combination.
+bool decode_supported(int dtype, int head_dim, int block_size, int group);
+bool cache_kernels_supported(int dtype, int head_dim, int block_size);
+
+}  // namespace vpa

@@ -1,0 +1,24 @@
+"""vpa — MI355X-native paged-KV hot path of the Qwen3-ASR decoder.
+
+Hand-written HIP kernels for gfx950 behind the C ABI of ``include/vpa.h``
+(``libvpa.so``), with the Candle-op-shaped tensor API of
+``mistralrs_paged_attn`` (as re-exported by ``vasr-paged-attn``) on top.
+"""
+
+from ._lib import VpaError  # noqa: F401
+from .ops import (  # noqa: F401
+    cache_geometry,
+    gather_kv_cache,
+    paged_attention,
+    paged_attention_workspace,
+    reshape_and_cache,
+)
+
+__all__ = [
+    "VpaError",
+    "cache_geometry",
+    "gather_kv_cache",
+    "paged_attention",
+    "paged_attention_workspace",
+    "reshape_and_cache",
+]

@@ -1,0 +1,84 @@
+"""ctypes binding of libvpa.so (the C ABI declared in include/vpa.h).
+
+The library is built in-tree by ``__graft_entry__.build()`` (or
+``make -C qwen3asr.rs_amd/csrc``) and must be present: there is no fallback
+path, a missing library raises immediately.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvpa.so")
+
+VPA_OK = 0
+VPA_ERR_INVALID_ARGUMENT = 1
+VPA_ERR_UNSUPPORTED = 2
+VPA_ERR_WORKSPACE = 3
+VPA_ERR_HIP = 4
+VPA_ERR_CAPACITY = 5
+VPA_ERR_NOT_FOUND = 6
+
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+DTYPE_BF16 = 2
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+_cstr = ctypes.c_char_p
+
+# name -> (restype, argtypes); mirrors include/vpa.h
+SIGNATURES = {
+    "vpa_last_error": (_cstr, []),
+    "vpa_version": (_cstr, []),
+    "vpa_cache_layout": (ctypes.c_int, [_i32, _i32, _i32, _i64, _i32, _p, _p]),
+    "vpa_reshape_and_cache": (ctypes.c_int, [_p, _p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i32,
+                                             _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
+    "vpa_paged_attention_workspace_size": (_sz, [_i32, _i32, _i32, _i32]),
+    "vpa_paged_attention": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _f32,
+                                           _f32, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i64,
+                                           _i64, _i32, _i32, _p, _sz, _p]),
+    "vpa_gather_kv_cache": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _i32, _i64, _i32,
+                                           _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
+}
+
+
+class VpaError(RuntimeError):
+    """A libvpa entry point returned a non-zero status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[vpa status {code}] {message}")
+        self.code = code
+        self.message = message
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libvpa.so once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"libvpa.so not found at {LIB_PATH}: build it with __graft_entry__.build() "
+            "(the paged-KV ops have no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(code: int) -> None:
+    if code != VPA_OK:
+        msg = load().vpa_last_error().decode("utf-8", "replace")
+        raise VpaError(code, msg)

@@ -1,0 +1,218 @@
+"""Tensor-level paged-KV ops over libvpa, mirroring the Candle op API.
+
+The three functions below keep the names, argument order, argument meaning
+and error behaviour of the ``mistralrs_paged_attn`` ops that vASR calls
+(re-exported at ``vasr-paged-attn/src/lib.rs:20-21``):
+
+* ``reshape_and_cache``  — ``vasr-models/src/model/thinker_text.rs:1101-1109, 1324-1332``
+* ``paged_attention``    — ``thinker_text.rs:1126-1139``
+* ``gather_kv_cache``    — ``thinker_text.rs:190-198, 1344-1352``
+
+plus ``paged_attention_varlen_prefill`` named after the reference's Metal
+paged prefill (``vasr-paged-attn/src/metal/varlen_prefill.rs:284-420``).
+
+Tensors are torch tensors on a ROCm device (torch is only the carrier of
+device memory and the current stream here); every computation runs in the
+HIP kernels of libvpa. Shape or dtype mismatches raise ``VpaError`` with
+status ``VPA_ERR_INVALID_ARGUMENT`` / ``VPA_ERR_UNSUPPORTED`` before any
+launch, as the reference returns ``Err(candle_core::Error::Msg)``.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import VpaError, check
+
+_DTYPES = {
+    torch.float32: _lib.DTYPE_F32,
+    torch.float16: _lib.DTYPE_F16,
+    torch.bfloat16: _lib.DTYPE_BF16,
+}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise VpaError(_lib.VPA_ERR_UNSUPPORTED, f"unsupported dtype {dtype}") from None
+
+
+def _err(msg: str):
+    return VpaError(_lib.VPA_ERR_INVALID_ARGUMENT, msg)
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require_device(*ts: torch.Tensor) -> None:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise _err(f"tensor on {t.device}: paged-KV ops run on the GPU only")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise _err(f"device mismatch: {dev} vs {t.device}")
+
+
+def cache_geometry(key_cache: torch.Tensor, value_cache: torch.Tensor):
+    """(num_blocks, num_kv_heads, head_dim, block_size, block_stride, head_stride)
+    of a key/value cache pair in the reference layout."""
+    if key_cache.dim() != 5 or value_cache.dim() != 4:
+        raise _err(f"key_cache must be 5-d and value_cache 4-d, got {tuple(key_cache.shape)} "
+                   f"and {tuple(value_cache.shape)}")
+    nb, kvh, dx, bs, x = key_cache.shape
+    nbv, kvhv, d, bsv = value_cache.shape
+    if (nb, kvh, bs) != (nbv, kvhv, bsv) or dx * x != d:
+        raise _err(f"paged cache shape mismatch: key={tuple(key_cache.shape)} "
+                   f"value={tuple(value_cache.shape)}")
+    if key_cache.dtype != value_cache.dtype:
+        raise _err(f"key/value cache dtype mismatch: {key_cache.dtype} vs {value_cache.dtype}")
+    if x * key_cache.element_size() != 16:
+        raise _err(f"key cache pack x={x} does not match 16 / {key_cache.element_size()}")
+    ks, vs = key_cache.stride(), value_cache.stride()
+    tile = d * bs
+    # (block, head) tiles must be contiguous; the two leading strides may be
+    # those of a view into a larger pool but must agree between K and V.
+    if ks[2:] != (bs * x, x, 1) or vs[2:] != (bs, 1):
+        raise _err("paged cache tiles must be contiguous")
+    if ks[0] != vs[0] or ks[1] != vs[1]:
+        raise _err(f"key/value cache strides differ: {ks[:2]} vs {vs[:2]}")
+    if ks[1] < tile:
+        raise _err(f"cache head stride {ks[1]} smaller than tile {tile}")
+    return nb, kvh, d, bs, ks[0], ks[1]
+
+
+def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_scale: Optional[torch.Tensor],
+                      v_scale: Optional[torch.Tensor], key_cache: torch.Tensor,
+                      value_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Scatter ``key``/``value`` [T, KVH, D] into the caches at ``slot_mapping`` (i64).
+
+    Negative slots are padding and are skipped. The caches are written in
+    place. ``k_scale``/``v_scale`` are accepted for signature parity and
+    ignored (no fp8 cache in this build)."""
+    _require_device(key, value, key_cache, value_cache, slot_mapping)
+    nb, kvh, d, bs, bstride, hstride = cache_geometry(key_cache, value_cache)
+    if key.dim() != 3 or value.shape != key.shape:
+        raise _err(f"key/value must be [T, KVH, D] of equal shape, got {tuple(key.shape)} and "
+                   f"{tuple(value.shape)}")
+    t, kh, kd = key.shape
+    if (kh, kd) != (kvh, d):
+        raise _err(f"key shape {tuple(key.shape)} does not match cache heads={kvh} dim={d}")
+    if key.dtype != value.dtype:
+        raise _err(f"key/value dtype mismatch: {key.dtype} vs {value.dtype}")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or slot_mapping.numel() != t:
+        raise _err(f"slot_mapping must be i64 [{t}], got {slot_mapping.dtype} "
+                   f"{tuple(slot_mapping.shape)}")
+    # Packed rows are used as they are; anything else is made contiguous
+    # (thinker_text.rs:43-62).
+    if key.stride(2) != 1 or key.stride(1) != d:
+        key = key.contiguous()
+    if value.stride(2) != 1 or value.stride(1) != d:
+        value = value.contiguous()
+    slot_mapping = slot_mapping.contiguous()
+    lib = _lib.load()
+    check(lib.vpa_reshape_and_cache(
+        key.data_ptr(), value.data_ptr(), key.stride(0), value.stride(0), _ptr(k_scale),
+        _ptr(v_scale), key_cache.data_ptr(), value_cache.data_ptr(), slot_mapping.data_ptr(), t,
+        kvh, d, bs, nb, bstride, hstride, dtype_code(key.dtype), dtype_code(key_cache.dtype),
+        _stream(key_cache)))
+
+
+def paged_attention_workspace(num_seqs: int, num_heads: int, head_dim: int,
+                              max_context_len: int, device) -> Optional[torch.Tensor]:
+    """Caller-side split-K workspace (None when not needed)."""
+    n = _lib.load().vpa_paged_attention_workspace_size(num_seqs, num_heads, head_dim,
+                                                        max_context_len)
+    if n == 0:
+        return None
+    # torch's caching allocator returns 512-byte aligned blocks
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def paged_attention(q: torch.Tensor, k_scale: Optional[torch.Tensor],
+                    v_scale: Optional[torch.Tensor], key_cache: torch.Tensor,
+                    value_cache: torch.Tensor, block_tables: torch.Tensor,
+                    context_lens: torch.Tensor, alibi_slopes: Optional[torch.Tensor],
+                    max_context_len: int, softmax_scale: float, softcapping: float,
+                    sinks: Optional[torch.Tensor], *, out: Optional[torch.Tensor] = None,
+                    workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Single-token decode attention over the paged cache; returns [B, H, D].
+
+    ``out`` and ``workspace`` are optional pre-allocated buffers (for callers
+    that capture the call in a HIP graph); otherwise they are allocated from
+    torch's caching allocator."""
+    _require_device(q, key_cache, value_cache, block_tables, context_lens)
+    nb, kvh, d, bs, bstride, hstride = cache_geometry(key_cache, value_cache)
+    if q.dim() != 3 or q.shape[2] != d:
+        raise _err(f"q must be [B, H, {d}], got {tuple(q.shape)}")
+    b, h, _ = q.shape
+    if block_tables.dtype != torch.uint32 or block_tables.dim() != 2 or block_tables.shape[0] != b:
+        raise _err(f"block_tables must be u32 [{b}, cols], got {block_tables.dtype} "
+                   f"{tuple(block_tables.shape)}")
+    if context_lens.dtype != torch.uint32 or context_lens.shape != (b,):
+        raise _err(f"context_lens must be u32 [{b}], got {context_lens.dtype} "
+                   f"{tuple(context_lens.shape)}")
+    q = q.contiguous()
+    block_tables = block_tables.contiguous()
+    context_lens = context_lens.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise _err("out must be a contiguous tensor shaped and typed like q")
+    lib = _lib.load()
+    need = lib.vpa_paged_attention_workspace_size(b, h, d, int(max_context_len))
+    if workspace is None and need > 0:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.vpa_paged_attention(
+        out.data_ptr(), q.data_ptr(), _ptr(k_scale), _ptr(v_scale), key_cache.data_ptr(),
+        value_cache.data_ptr(), block_tables.data_ptr(), block_tables.shape[1],
+        context_lens.data_ptr(), _ptr(alibi_slopes), int(max_context_len), float(softmax_scale),
+        float(softcapping), _ptr(sinks), b, h, kvh, d, bs, nb, bstride, hstride,
+        dtype_code(q.dtype), dtype_code(key_cache.dtype), _ptr(workspace), ws_bytes,
+        _stream(q)))
+    return out
+
+
+def gather_kv_cache(key_cache: torch.Tensor, value_cache: torch.Tensor,
+                    k_scale: Optional[torch.Tensor], v_scale: Optional[torch.Tensor],
+                    block_tables: torch.Tensor, cu_seqlens_kv: torch.Tensor,
+                    out_dtype: torch.dtype, *, total_tokens: Optional[int] = None
+                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Gather each sequence's tokens into packed K, V [sum(kv_lens), KVH, D].
+
+    ``total_tokens`` (= cu_seqlens_kv[-1]) may be given by a caller that
+    knows the lengths on the host; otherwise it is read from the device."""
+    _require_device(key_cache, value_cache, block_tables, cu_seqlens_kv)
+    nb, kvh, d, bs, bstride, hstride = cache_geometry(key_cache, value_cache)
+    if block_tables.dtype != torch.uint32 or block_tables.dim() != 2:
+        raise _err(f"block_tables must be u32 2-d, got {block_tables.dtype} "
+                   f"{tuple(block_tables.shape)}")
+    num_seqs = block_tables.shape[0]
+    if cu_seqlens_kv.dtype != torch.uint32 or cu_seqlens_kv.shape != (num_seqs + 1,):
+        raise _err(f"cu_seqlens_kv must be u32 [{num_seqs + 1}], got {cu_seqlens_kv.dtype} "
+                   f"{tuple(cu_seqlens_kv.shape)}")
+    if total_tokens is None:
+        total_tokens = int(cu_seqlens_kv[-1].item())
+    block_tables = block_tables.contiguous()
+    cu_seqlens_kv = cu_seqlens_kv.contiguous()
+    out_k = torch.empty((total_tokens, kvh, d), dtype=out_dtype, device=key_cache.device)
+    out_v = torch.empty_like(out_k)
+    check(_lib.load().vpa_gather_kv_cache(
+        out_k.data_ptr(), out_v.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+        _ptr(k_scale), _ptr(v_scale), block_tables.data_ptr(), block_tables.shape[1],
+        cu_seqlens_kv.data_ptr(), num_seqs, total_tokens, kvh, d, bs, nb, bstride, hstride,
+        dtype_code(key_cache.dtype), dtype_code(out_dtype), _stream(key_cache)))
+    return out_k, out_v

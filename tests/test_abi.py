@@ -1,0 +1,163 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+declared in include/vpa.h, and rejects bad arguments on the host before any
+launch (so these calls never touch a device)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from vpa import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            src = open(os.path.join(ROOT, "include", fn)).read()
+            src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+            names.update(re.findall(r"\b(vpa_[a-z0-9_]+)\s*\(", src))
+    return sorted(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert "vpa_paged_attention" in names and "vpa_reshape_and_cache" in names
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_version_and_empty_error():
+    lib = _lib.load()
+    assert lib.vpa_version().startswith(b"vpa")
+
+
+def layout(kvh, d, bs, nb, dtype):
+    ks = (ctypes.c_int64 * 5)()
+    vs = (ctypes.c_int64 * 4)()
+    rc = _lib.load().vpa_cache_layout(kvh, d, bs, nb, dtype, ks, vs)
+    return rc, tuple(ks), tuple(vs)
+
+
+def test_cache_layout_matches_reference_kat():
+    # PagedKvCache::new(1, 2, 8, 4, 10, F32): 3 blocks, key [3,2,2,4,4],
+    # value [3,2,8,4] (vasr-paged-attn/src/paged_kv_cache.rs:1091-1107)
+    rc, ks, vs = layout(2, 8, 4, 3, _lib.DTYPE_F32)
+    assert rc == 0
+    assert ks == (3, 2, 2, 4, 4)
+    assert vs == (3, 2, 8, 4)
+    rc, ks, vs = layout(8, 128, 16, 100, _lib.DTYPE_BF16)
+    assert rc == 0 and ks == (100, 8, 16, 16, 8) and vs == (100, 8, 128, 16)
+
+
+@pytest.mark.parametrize("args,code,needle", [
+    ((0, 8, 4, 3, 0), _lib.VPA_ERR_INVALID_ARGUMENT, "kv head"),
+    ((2, 0, 4, 3, 0), _lib.VPA_ERR_INVALID_ARGUMENT, "head_dim"),
+    ((2, 8, 0, 3, 0), _lib.VPA_ERR_INVALID_ARGUMENT, "block_size"),
+    ((2, 8, 4, 0, 0), _lib.VPA_ERR_INVALID_ARGUMENT, "num_blocks"),
+    ((2, 12, 4, 3, 2), _lib.VPA_ERR_INVALID_ARGUMENT, "divisible by key cache pack size"),
+    ((2, 8, 4, 3, 9), _lib.VPA_ERR_UNSUPPORTED, "dtype"),
+])
+def test_cache_layout_rejects(args, code, needle):
+    rc, _, _ = layout(*args)
+    assert rc == code
+    assert needle in _lib.load().vpa_last_error().decode()
+
+
+FAKE = 1 << 20  # 16-byte aligned non-null host values standing in for device pointers
+
+
+def rc_call(**over):
+    args = dict(key=FAKE, value=FAKE, kts=1024, vts=1024, ks=None, vs=None, kc=FAKE, vc=FAKE,
+                slots=FAKE, t=4, kvh=8, d=128, bs=16, nb=10, bstride=8 * 128 * 16,
+                hstride=128 * 16, dtype=_lib.DTYPE_BF16, cdtype=_lib.DTYPE_BF16, stream=None)
+    args.update(over)
+    lib = _lib.load()
+    rc = lib.vpa_reshape_and_cache(*args.values())
+    return rc, lib.vpa_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,needle", [
+    (dict(dtype=_lib.DTYPE_F32), _lib.VPA_ERR_UNSUPPORTED, "differs"),
+    (dict(dtype=7, cdtype=7), _lib.VPA_ERR_UNSUPPORTED, "dtype"),
+    (dict(d=96), _lib.VPA_ERR_UNSUPPORTED, "no kernel"),
+    (dict(bs=24), _lib.VPA_ERR_UNSUPPORTED, "no kernel"),
+    (dict(hstride=100), _lib.VPA_ERR_INVALID_ARGUMENT, "strides"),
+    (dict(bstride=128 * 16), _lib.VPA_ERR_INVALID_ARGUMENT, "strides"),
+    (dict(kts=512), _lib.VPA_ERR_INVALID_ARGUMENT, "token stride"),
+    (dict(slots=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
+    (dict(kc=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
+    (dict(key=FAKE + 2), _lib.VPA_ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(t=-1), _lib.VPA_ERR_INVALID_ARGUMENT, "num_tokens"),
+    (dict(nb=0), _lib.VPA_ERR_INVALID_ARGUMENT, "positive"),
+])
+def test_reshape_and_cache_host_validation(over, code, needle):
+    rc, msg = rc_call(**over)
+    assert rc == code, msg
+    assert needle in msg
+
+
+def test_reshape_and_cache_zero_tokens_is_noop():
+    rc, _ = rc_call(t=0, key=None, value=None, slots=None)
+    assert rc == 0
+
+
+def pa_call(**over):
+    args = dict(out=FAKE, q=FAKE, ks=None, vs=None, kc=FAKE, vc=FAKE, bt=FAKE, bts=64, cl=FAKE,
+                alibi=None, max_ctx=1024, scale=0.088, softcap=1.0, sinks=None, b=4, h=16, kvh=8,
+                d=128, bs=16, nb=100, bstride=8 * 128 * 16, hstride=128 * 16,
+                dtype=_lib.DTYPE_BF16, cdtype=_lib.DTYPE_BF16, ws=None, ws_bytes=0, stream=None)
+    args.update(over)
+    lib = _lib.load()
+    rc = lib.vpa_paged_attention(*args.values())
+    return rc, lib.vpa_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,needle", [
+    (dict(alibi=FAKE), _lib.VPA_ERR_UNSUPPORTED, "alibi"),
+    (dict(sinks=FAKE), _lib.VPA_ERR_UNSUPPORTED, "sinks"),
+    (dict(softcap=30.0), _lib.VPA_ERR_UNSUPPORTED, "softcapping"),
+    (dict(h=12), _lib.VPA_ERR_INVALID_ARGUMENT, "multiple"),
+    (dict(h=64), _lib.VPA_ERR_UNSUPPORTED, "query heads per kv head"),
+    (dict(bts=10), _lib.VPA_ERR_INVALID_ARGUMENT, "block_table_stride"),
+    (dict(q=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
+    (dict(cdtype=_lib.DTYPE_F16), _lib.VPA_ERR_UNSUPPORTED, "differs"),
+    (dict(), _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(ws=FAKE + 16, ws_bytes=1 << 30), _lib.VPA_ERR_INVALID_ARGUMENT, "256-byte"),
+    (dict(max_ctx=1 << 30, bts=1 << 26), _lib.VPA_ERR_UNSUPPORTED, "max_context_len"),
+])
+def test_paged_attention_host_validation(over, code, needle):
+    rc, msg = pa_call(**over)
+    assert rc == code, msg
+    assert needle in msg
+
+
+def test_paged_attention_workspace_size():
+    lib = _lib.load()
+    # a single partition (<= 256 tokens) needs no workspace
+    assert lib.vpa_paged_attention_workspace_size(256, 16, 128, 256) == 0
+    n = lib.vpa_paged_attention_workspace_size(256, 16, 128, 4096)
+    rows = 256 * 16 * 16
+    assert n >= rows * 128 * 4 + 2 * rows * 4
+    assert pa_call(b=0)[0] == 0  # empty batch: no launch, no workspace
+
+
+def test_gather_host_validation():
+    lib = _lib.load()
+    rc = lib.vpa_gather_kv_cache(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, 4, FAKE, 2, 10, 8, 128,
+                                 16, 100, 8 * 128 * 16, 128 * 16, _lib.DTYPE_BF16, _lib.DTYPE_F32,
+                                 None)
+    assert rc == _lib.VPA_ERR_UNSUPPORTED
+    rc = lib.vpa_gather_kv_cache(None, FAKE, FAKE, FAKE, None, None, FAKE, 4, FAKE, 2, 10, 8, 128,
+                                 16, 100, 8 * 128 * 16, 128 * 16, _lib.DTYPE_BF16,
+                                 _lib.DTYPE_BF16, None)
+    assert rc == _lib.VPA_ERR_INVALID_ARGUMENT
+    rc = lib.vpa_gather_kv_cache(None, None, FAKE, FAKE, None, None, None, 4, None, 0, 0, 8, 128,
+                                 16, 100, 8 * 128 * 16, 128 * 16, _lib.DTYPE_BF16,
+                                 _lib.DTYPE_BF16, None)
+    assert rc == 0

@@ -1,0 +1,217 @@
+"""GPU parity of paged_attention (decode) against the fp64 oracle.
+
+Tolerances (from the acceptance bar): relative 1e-5 for f32, 2e-2 for bf16 and
+f16, element-wise with a floor of tol/10 of the largest output magnitude (see
+tests/_util.assert_attention_close)."""
+
+import numpy as np
+import pytest
+import torch
+
+import vpa
+from oracle import oracle as orc
+from tests._util import (assert_attention_close, block_tables_for, i64, make_cache,
+                         random_words, to_dev, to_host, u32)
+
+pytestmark = pytest.mark.gpu
+
+
+def decode_case(device, code, h, kvh, d, bs, lens, seed, nb=None, pad_cols=0, max_ctx=None,
+                mutate_bt=None, scale=None):
+    rng = np.random.default_rng(seed)
+    need = sum((int(L) + bs - 1) // bs for L in lens)
+    nb = nb or need + 8
+    kc, vc = make_cache(rng, nb, kvh, d, bs, code)
+    bt = block_tables_for(rng, [max(int(L), 1) for L in lens], nb, bs, pad_cols=pad_cols)
+    if mutate_bt is not None:
+        mutate_bt(bt)
+    q = random_words(rng, (len(lens), h, d), code)
+    lens = np.asarray(lens, dtype=np.uint32)
+    max_ctx = int(lens.max()) if max_ctx is None else max_ctx
+    scale = d ** -0.5 if scale is None else scale
+    out = vpa.paged_attention(to_dev(q, code, device), None, None, to_dev(kc, code, device),
+                              to_dev(vc, code, device), u32(bt, device), u32(lens, device), None,
+                              max_ctx, scale, 1.0, None)
+    torch.cuda.synchronize()
+    want = orc.paged_attention(q, kc, vc, bt, lens, max_ctx, scale, dtype=code)
+    got = orc.to_f32(to_host(out), code)
+    return got, want
+
+
+@pytest.mark.parametrize("code", [orc.F32, orc.BF16, orc.F16])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_decode_qwen3_asr_shape(device, code, bs):
+    lens = [1, 2, 15, 16, 17, 100, 255, 256, 257, 511, 512, 600, 1300]
+    got, want = decode_case(device, code, 16, 8, 128, bs, lens, seed=bs + 3 * code)
+    assert_attention_close(got, want, code, f"code={code} bs={bs}")
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("h,kvh", [(8, 8), (16, 8), (16, 4)])
+@pytest.mark.parametrize("code", [orc.BF16, orc.F32])
+def test_decode_head_dims_and_groups(device, d, h, kvh, code):
+    lens = [3, 64, 300, 777]
+    got, want = decode_case(device, code, h, kvh, d, 16, lens, seed=d + h + kvh)
+    assert_attention_close(got, want, code, f"d={d} h={h} kvh={kvh}")
+
+
+def test_decode_config_c1(device):
+    """c1: f32, one sequence of 512 tokens in 32 blocks of a 64-block pool."""
+    from vpa import workloads
+    w = workloads.c1()
+    rng = np.random.default_rng(w.seed)
+    code = orc.F32
+    kc, vc = make_cache(rng, 64, 8, 128, 16, code, zero=True)
+    bt = w.layers[0].block_tables
+    pos = np.arange(512)
+    slots = bt[0, pos // 16].astype(np.int64) * 16 + pos % 16
+    k = (rng.standard_normal((512, 8, 128)) / np.sqrt(128)).astype(np.float32)
+    v = (rng.standard_normal((512, 8, 128)) / np.sqrt(128)).astype(np.float32)
+    q = (rng.standard_normal((1, 16, 128)) / np.sqrt(128)).astype(np.float32)
+    kc_d, vc_d = to_dev(kc, code, device), to_dev(vc, code, device)
+    # prefill 0..510, then the decode append at 511
+    vpa.reshape_and_cache(to_dev(k[:511], code, device), to_dev(v[:511], code, device), None, None,
+                          kc_d, vc_d, i64(slots[:511], device))
+    vpa.reshape_and_cache(to_dev(k[511:], code, device), to_dev(v[511:], code, device), None, None,
+                          kc_d, vc_d, i64(w.layers[0].slot_mapping, device))
+    out = vpa.paged_attention(to_dev(q, code, device), None, None, kc_d, vc_d, u32(bt, device),
+                              u32(w.context_lens, device), None, 512, 128 ** -0.5, 1.0, None)
+    torch.cuda.synchronize()
+    orc.reshape_and_cache(k, v, kc, vc, slots, dtype=code)
+    np.testing.assert_array_equal(to_host(kc_d), kc)
+    want = orc.paged_attention(q, kc, vc, bt, w.context_lens, 512, 128 ** -0.5, dtype=code)
+    assert_attention_close(to_host(out), want, code, "c1")
+
+
+def test_decode_config_c2(device):
+    """c2: bf16, B=32, L~U[100,1500], shuffled pool with 25% slack."""
+    from vpa import workloads
+    w = workloads.c2()
+    code = orc.BF16
+    layer = w.layers[0]
+    rng = np.random.default_rng(w.seed)
+    kc, vc = make_cache(rng, layer.num_blocks, 8, 128, 16, code)
+    q = random_words(rng, (32, 16, 128), code)
+    nk = random_words(rng, (32, 8, 128), code)
+    nv = random_words(rng, (32, 8, 128), code)
+    kc_d, vc_d = to_dev(kc, code, device), to_dev(vc, code, device)
+    vpa.reshape_and_cache(to_dev(nk, code, device), to_dev(nv, code, device), None, None, kc_d,
+                          vc_d, i64(layer.slot_mapping, device))
+    out = vpa.paged_attention(to_dev(q, code, device), None, None, kc_d, vc_d,
+                              u32(layer.block_tables, device), u32(w.context_lens, device), None,
+                              w.max_context_len, 128 ** -0.5, 1.0, None)
+    torch.cuda.synchronize()
+    orc.reshape_and_cache(nk, nv, kc, vc, layer.slot_mapping, dtype=code)
+    np.testing.assert_array_equal(to_host(kc_d), kc)
+    np.testing.assert_array_equal(to_host(vc_d), vc)
+    want = orc.paged_attention(q, kc, vc, layer.block_tables, w.context_lens, w.max_context_len,
+                               128 ** -0.5, dtype=code)
+    assert_attention_close(orc.to_f32(to_host(out), code), want, code, "c2")
+
+
+def test_decode_long_context_split_k(device):
+    """Contexts spanning many split-K partitions (up to 8192 tokens)."""
+    lens = [8192, 4097, 4096, 2049, 333]
+    got, want = decode_case(device, orc.BF16, 16, 8, 128, 16, lens, seed=77)
+    assert_attention_close(got, want, orc.BF16, "long")
+
+
+def test_decode_max_context_len_above_lengths_and_padded_columns(device):
+    """max_context_len frozen above every length (graph-capture style) and
+    block tables padded with 0 columns (paged_kv_cache.rs:954-964) or a
+    repeated tail (cuda_graph.rs:471-486)."""
+    lens = [40, 700, 1]
+
+    def repeat_tail(bt):
+        for s, L in enumerate(lens):
+            n = (L + 15) // 16
+            bt[s, n:] = bt[s, n - 1]
+
+    got, want = decode_case(device, orc.BF16, 16, 8, 128, 16, lens, seed=5, pad_cols=70,
+                            max_ctx=(44 + 70) * 16)
+    assert_attention_close(got, want, orc.BF16, "zero-padded")
+    got, want = decode_case(device, orc.BF16, 16, 8, 128, 16, lens, seed=6, pad_cols=70,
+                            max_ctx=(44 + 70) * 16, mutate_bt=repeat_tail)
+    assert_attention_close(got, want, orc.BF16, "tail-padded")
+
+
+def test_decode_graph_padding_rows(device):
+    """Padded rows of a captured batch: context 1, block 0 (cuda_graph.rs:395-408)."""
+    lens = [300, 1, 1, 1]
+
+    def pad_rows(bt):
+        bt[1:] = 0
+
+    got, want = decode_case(device, orc.BF16, 16, 8, 128, 16, lens, seed=9, mutate_bt=pad_rows)
+    assert_attention_close(got, want, orc.BF16, "pad rows")
+
+
+def test_decode_invalid_block_ids_are_skipped(device):
+    lens = [100, 520]
+
+    def corrupt(bt):
+        bt[0, 2] = 1 << 30
+        bt[1, 17] = 0xFFFFFFFF
+
+    got, want = decode_case(device, orc.F32, 16, 8, 128, 16, lens, seed=12, mutate_bt=corrupt)
+    assert_attention_close(got, want, orc.F32, "invalid blocks")
+
+
+def test_decode_stale_nan_past_context_is_ignored(device):
+    """Cache contents past a sequence's length (here NaN) must not leak in."""
+    rng = np.random.default_rng(31)
+    code, nb = orc.F32, 8
+    kc, vc = make_cache(rng, nb, 8, 128, 16, code)
+    bt = np.array([[3, 5]], dtype=np.uint32)
+    kc[5, :, :, 4:, :] = np.nan
+    vc[5, :, :, 4:] = np.nan
+    q = random_words(rng, (1, 16, 128), code)
+    lens = np.array([20], dtype=np.uint32)
+    out = vpa.paged_attention(to_dev(q, code, device), None, None, to_dev(kc, code, device),
+                              to_dev(vc, code, device), u32(bt, device), u32(lens, device), None,
+                              20, 0.1, 1.0, None)
+    torch.cuda.synchronize()
+    want = orc.paged_attention(q, kc, vc, bt, lens, 20, 0.1, dtype=code)
+    assert_attention_close(to_host(out), want, code, "stale nan")
+
+
+def test_decode_zero_context_gives_zeros(device):
+    got, want = decode_case(device, orc.BF16, 16, 8, 128, 16, [0, 50], seed=2)
+    assert not got[0].any()
+    assert_attention_close(got, want, orc.BF16, "ctx0")
+
+
+def test_decode_matches_across_partition_counts(device):
+    """Split-K must not change results: one long sequence against the same
+    tokens attended with max_context_len raised (more, emptier partitions)."""
+    a, want = decode_case(device, orc.F32, 16, 8, 128, 16, [3000], seed=4)
+    b, _ = decode_case(device, orc.F32, 16, 8, 128, 16, [3000], seed=4, pad_cols=200,
+                       max_ctx=3000 + 200 * 16)
+    np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-7)
+    assert_attention_close(a, want, orc.F32, "split")
+
+
+def test_decode_preallocated_out_and_workspace(device):
+    rng = np.random.default_rng(1)
+    code = orc.BF16
+    lens = np.array([900, 30], dtype=np.uint32)
+    nb = 80
+    kc, vc = make_cache(rng, nb, 8, 128, 16, code)
+    bt = block_tables_for(rng, lens, nb, 16)
+    q = random_words(rng, (2, 16, 128), code)
+    qd = to_dev(q, code, device)
+    ws = vpa.paged_attention_workspace(2, 16, 128, 900, device)
+    assert ws is not None
+    out = torch.empty_like(qd)
+    res = vpa.paged_attention(qd, None, None, to_dev(kc, code, device), to_dev(vc, code, device),
+                              u32(bt, device), u32(lens, device), None, 900, 0.088, 1.0, None,
+                              out=out, workspace=ws)
+    torch.cuda.synchronize()
+    assert res.data_ptr() == out.data_ptr()
+    want = orc.paged_attention(q, kc, vc, bt, lens, 900, 0.088, dtype=code)
+    assert_attention_close(orc.to_f32(to_host(out), code), want, code, "prealloc")
+    with pytest.raises(vpa.VpaError) as e:
+        vpa.paged_attention(qd, None, None, to_dev(kc, code, device), to_dev(vc, code, device),
+                            u32(bt, device), u32(lens, device), None, 900, 0.088, 1.0, None,
+                            workspace=ws[:100])
+    assert e.value.code == 3

@@ -1,0 +1,349 @@
+"""Pins of the CPU oracle (oracle/vpa_oracle.c) — CPU only.
+
+Each check is chosen so that a plausible slip in the oracle (a transposed
+tile, a wrong GQA map, a missing 1e-6, a shifted causal diagonal) fails it,
+and none retypes the oracle's own formula:
+
+* cache layout: the reference's host-side inverse of the layout
+  (``vasr-models/src/model/generation.rs:338-440``: transpose(0,1),
+  transpose(2,3), reshape) applied with numpy transposes;
+* reshape_and_cache: PAD_SLOT_ID skip (``paged_kv_cache.rs:697-700``),
+  canary bytes outside the target slots, bit patterns (NaN payloads)
+  preserved;
+* gather_kv_cache: append -> gather round trip;
+* decode and prefill attention: torch's scaled_dot_product_attention (a
+  library routine) on the gathered K/V with repeat_interleave GQA, and the
+  1e-6 term pinned through torch.logsumexp; closed forms (L=1, constant keys,
+  one-hot values revealing the causal mask of ``attention.rs:78-149``, KAT
+  ``attention.rs:870-909``); the reference's packed-vs-unpacked test inputs
+  (``attention.rs:949-1041``, q=i*0.01, kv=i*0.02+1, tolerance 1e-4);
+  physical-block permutation invariance.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.filterwarnings("ignore::UserWarning")
+
+
+def make_cache(nb, kvh, d, bs, code, rng, fill=None):
+    x = 16 // (4 if code == orc.F32 else 2)
+    kshape = (nb, kvh, d // x, bs, x)
+    vshape = (nb, kvh, d, bs)
+    if fill is None:
+        k = orc.from_f32(rng.standard_normal(kshape).astype(np.float32), code)
+        v = orc.from_f32(rng.standard_normal(vshape).astype(np.float32), code)
+    else:
+        dt = np.float32 if code == orc.F32 else np.uint16
+        k = np.full(kshape, fill, dtype=dt)
+        v = np.full(vshape, fill, dtype=dt)
+    return np.ascontiguousarray(k), np.ascontiguousarray(v)
+
+
+def inverse_layout(key_cache, value_cache, table, length):
+    """Host inverse of the paged layout as the reference writes it
+    (generation.rs:338-440): per sequence, cat the blocks of its table, then
+    K: transpose(0,1).transpose(2,3).reshape(KVH, NB*BS, D)[:, :len];
+    V: the same on [NB, KVH, D, BS]."""
+    kb = key_cache[np.asarray(table)]            # [nb, KVH, D/x, BS, x]
+    vb = value_cache[np.asarray(table)]          # [nb, KVH, D, BS]
+    nbk, kvh, dx, bs, x = kb.shape
+    k = kb.transpose(1, 0, 2, 3, 4).transpose(0, 1, 3, 2, 4).reshape(kvh, nbk * bs, dx * x)
+    v = vb.transpose(1, 0, 2, 3).transpose(0, 1, 3, 2).reshape(kvh, nbk * bs, dx * x)
+    return k[:, :length], v[:, :length]
+
+
+@pytest.mark.parametrize("code", [orc.F32, orc.BF16, orc.F16])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_reshape_and_cache_matches_reference_inverse(code, bs):
+    rng = np.random.default_rng(10 + bs + code)
+    kvh, d, nb = 2, 64, 24
+    length = 3 * bs + 5
+    table = rng.permutation(nb)[: (length + bs - 1) // bs]
+    kc, vc = make_cache(nb, kvh, d, bs, code, rng, fill=0)
+    k = orc.from_f32(rng.standard_normal((length, kvh, d)).astype(np.float32), code)
+    v = orc.from_f32(rng.standard_normal((length, kvh, d)).astype(np.float32), code)
+    pos = np.arange(length)
+    slots = table[pos // bs].astype(np.int64) * bs + pos % bs
+    orc.reshape_and_cache(k, v, kc, vc, slots, dtype=code)
+    ki, vi = inverse_layout(kc, vc, table, length)
+    np.testing.assert_array_equal(ki, k.transpose(1, 0, 2))
+    np.testing.assert_array_equal(vi, v.transpose(1, 0, 2))
+
+
+def test_reshape_and_cache_pad_slots_and_canary():
+    rng = np.random.default_rng(7)
+    kvh, d, bs, nb = 2, 64, 16, 8
+    kc, vc = make_cache(nb, kvh, d, bs, orc.BF16, rng, fill=0xABCD)
+    k0, v0 = kc.copy(), vc.copy()
+    # random words including NaN/Inf bit patterns: the copy must keep them
+    k = rng.integers(0, 1 << 16, size=(6, kvh, d), dtype=np.uint16)
+    v = rng.integers(0, 1 << 16, size=(6, kvh, d), dtype=np.uint16)
+    k[0, 0, :4] = [0x7FC1, 0xFF80, 0x7F80, 0x0001]
+    slots = np.array([5, -1, 17, nb * bs, 127, -7], dtype=np.int64)  # -1/-7 pad, nb*bs out of range
+    orc.reshape_and_cache(k, v, kc, vc, slots, dtype=orc.BF16)
+    x = 8
+    touched_k = np.zeros(kc.shape, dtype=bool)
+    touched_v = np.zeros(vc.shape, dtype=bool)
+    for t, s in enumerate(slots):
+        if s < 0 or s >= nb * bs:
+            continue
+        blk, off = divmod(int(s), bs)
+        for j in range(kvh):
+            for dd in range(d):
+                assert kc[blk, j, dd // x, off, dd % x] == k[t, j, dd]
+                assert vc[blk, j, dd, off] == v[t, j, dd]
+                touched_k[blk, j, dd // x, off, dd % x] = True
+                touched_v[blk, j, dd, off] = True
+    assert touched_k.sum() == 3 * kvh * d
+    np.testing.assert_array_equal(kc[~touched_k], k0[~touched_k])
+    np.testing.assert_array_equal(vc[~touched_v], v0[~touched_v])
+
+
+@pytest.mark.parametrize("code", [orc.F32, orc.BF16])
+def test_gather_round_trip(code):
+    rng = np.random.default_rng(3)
+    kvh, d, bs, nb = 2, 64, 16, 40
+    lens = np.array([37, 1, 16, 50])
+    kc, vc = make_cache(nb, kvh, d, bs, code, rng)
+    perm = rng.permutation(np.arange(1, nb))
+    cols = int(max((lens + bs - 1) // bs))
+    bt = np.zeros((len(lens), cols), dtype=np.uint32)
+    rows_k, rows_v, slots = [], [], []
+    off = 0
+    for s, L in enumerate(lens):
+        n = (L + bs - 1) // bs
+        bt[s, :n] = perm[off:off + n]
+        off += n
+        pos = np.arange(L)
+        slots.append(bt[s, pos // bs].astype(np.int64) * bs + pos % bs)
+        rows_k.append(orc.from_f32(rng.standard_normal((L, kvh, d)).astype(np.float32), code))
+        rows_v.append(orc.from_f32(rng.standard_normal((L, kvh, d)).astype(np.float32), code))
+    k = np.ascontiguousarray(np.concatenate(rows_k))
+    v = np.ascontiguousarray(np.concatenate(rows_v))
+    orc.reshape_and_cache(k, v, kc, vc, np.concatenate(slots), dtype=code)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    gk, gv = orc.gather_kv_cache(kc, vc, bt, cu, dtype=code)
+    np.testing.assert_array_equal(gk, k)
+    np.testing.assert_array_equal(gv, v)
+
+
+def _random_decode(rng, code, b, h, kvh, d, bs, lens, nb):
+    kc, vc = make_cache(nb, kvh, d, bs, code, rng)
+    cols = int(max((np.asarray(lens) + bs - 1) // bs))
+    bt = np.zeros((b, cols), dtype=np.uint32)
+    for s, L in enumerate(lens):
+        n = (L + bs - 1) // bs
+        bt[s, :n] = rng.choice(nb, size=n, replace=False)
+    q = orc.from_f32(rng.standard_normal((b, h, d)).astype(np.float32), code)
+    return q, kc, vc, bt
+
+
+def _sdpa_decode(q, kc, vc, bt, lens, scale, code):
+    """torch SDPA (float64, CPU) on K/V recovered with the reference inverse."""
+    b, h, d = q.shape
+    kvh = kc.shape[1]
+    outs, lse = [], []
+    for s, L in enumerate(lens):
+        n = (L + kc.shape[3] - 1) // kc.shape[3]
+        ki, vi = inverse_layout(kc, vc, bt[s, :n], L)
+        K = torch.from_numpy(orc.to_f32(ki, code).astype(np.float64))
+        V = torch.from_numpy(orc.to_f32(vi, code).astype(np.float64))
+        K = K.repeat_interleave(h // kvh, dim=0)
+        V = V.repeat_interleave(h // kvh, dim=0)
+        Q = torch.from_numpy(orc.to_f32(q[s], code).astype(np.float64))[:, None, :]
+        o = torch.nn.functional.scaled_dot_product_attention(Q, K, V, scale=scale)[:, 0, :]
+        logits = (Q @ K.transpose(1, 2))[:, 0, :] * scale
+        m = logits.max(dim=1, keepdim=True).values
+        S = torch.exp(torch.logsumexp(logits, dim=1, keepdim=True) - m)  # sum exp(s - max)
+        outs.append(o)
+        lse.append(S)
+    return torch.stack(outs).numpy(), torch.stack(lse).numpy()
+
+
+@pytest.mark.parametrize("code,h,kvh,bs", [(orc.F32, 16, 8, 16), (orc.BF16, 16, 8, 16),
+                                           (orc.F16, 8, 2, 8), (orc.F32, 4, 4, 32)])
+def test_decode_oracle_matches_torch_sdpa(code, h, kvh, bs):
+    rng = np.random.default_rng(100 + h + bs)
+    d, nb = 128, 96
+    lens = [1, 17, 200, 333]
+    q, kc, vc, bt = _random_decode(rng, code, len(lens), h, kvh, d, bs, lens, nb)
+    scale = d ** -0.5
+    got = orc.paged_attention(q, kc, vc, bt, np.array(lens), max(lens), scale, dtype=code)
+    want, S = _sdpa_decode(q, kc, vc, bt, lens, scale, code)
+    # the oracle divides by (S + 1e-6); SDPA by S
+    np.testing.assert_allclose(got * (S + 1e-6) / S, want, rtol=1e-10, atol=1e-12)
+
+
+def test_decode_closed_forms():
+    rng = np.random.default_rng(5)
+    code, h, kvh, d, bs, nb = orc.F32, 4, 2, 64, 16, 16
+    # L = 1: out = V[t0] / (1 + 1e-6)
+    q, kc, vc, bt = _random_decode(rng, code, 1, h, kvh, d, bs, [1], nb)
+    out = orc.paged_attention(q, kc, vc, bt, np.array([1]), 1, 0.1, dtype=code)
+    for hh in range(h):
+        v0 = vc[bt[0, 0], hh // 2, :, 0].astype(np.float64)
+        np.testing.assert_allclose(out[0, hh], v0 / (1 + 1e-6), rtol=1e-12)
+    # constant keys: uniform weights -> mean of V * L/(L+1e-6)
+    L = 40
+    q, kc, vc, bt = _random_decode(rng, code, 1, h, kvh, d, bs, [L], nb)
+    kc[:] = 0.25
+    out = orc.paged_attention(q, kc, vc, bt, np.array([L]), L, 0.3, dtype=code)
+    _, vi = inverse_layout(kc, vc, bt[0, :3], L)
+    for hh in range(h):
+        np.testing.assert_allclose(out[0, hh], vi[hh // 2].astype(np.float64).mean(0) * L / (L + 1e-6),
+                                   rtol=1e-10)
+
+
+def test_decode_permutation_invariance_and_invalid_blocks():
+    rng = np.random.default_rng(9)
+    code, h, kvh, d, bs, nb = orc.BF16, 16, 8, 128, 16, 32
+    L = 70
+    q, kc, vc, bt = _random_decode(rng, code, 1, h, kvh, d, bs, [L], nb)
+    base = orc.paged_attention(q, kc, vc, bt, np.array([L]), L, 0.088, dtype=code)
+    perm = rng.permutation(nb)
+    kc2, vc2 = np.empty_like(kc), np.empty_like(vc)
+    kc2[perm] = kc
+    vc2[perm] = vc
+    bt2 = perm[bt].astype(np.uint32)
+    moved = orc.paged_attention(q, kc2, vc2, bt2, np.array([L]), L, 0.088, dtype=code)
+    np.testing.assert_allclose(moved, base, rtol=1e-12, atol=1e-15)
+    # a block id >= num_blocks drops that block's tokens: same as attending to
+    # the remaining tokens only (here: tokens 16..69 after moving block 0 out)
+    bt3 = bt.copy()
+    bt3[0, 0] = nb + 5
+    part = orc.paged_attention(q, kc, vc, bt3, np.array([L]), L, 0.088, dtype=code)
+    ki, vi = inverse_layout(kc, vc, bt[0, :5], L)
+    Q = orc.to_f32(q[0], code).astype(np.float64)
+    K = orc.to_f32(ki, code).astype(np.float64)[:, 16:]
+    V = orc.to_f32(vi, code).astype(np.float64)[:, 16:]
+    for hh in range(h):
+        lg = K[hh // 2] @ Q[hh] * 0.088
+        p = np.exp(lg - lg.max())
+        np.testing.assert_allclose(part[0, hh], p @ V[hh // 2] / (p.sum() + 1e-6), rtol=1e-10)
+
+
+def _prefill_case(rng, code, h, kvh, d, bs, prior, qlens, nb):
+    lens = np.asarray(prior) + np.asarray(qlens)
+    kc, vc = make_cache(nb, kvh, d, bs, code, rng)
+    cols = int(max((lens + bs - 1) // bs))
+    bt = np.zeros((len(lens), cols), dtype=np.uint32)
+    ids = rng.permutation(nb)
+    off = 0
+    for s, L in enumerate(lens):
+        n = (L + bs - 1) // bs
+        bt[s, :n] = ids[off:off + n]
+        off += n
+    tq = int(sum(qlens))
+    q = orc.from_f32(rng.standard_normal((tq, h, d)).astype(np.float32), code)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.uint32)
+    return q, kc, vc, bt, lens.astype(np.uint32), cu
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_oracle_matches_torch_sdpa_with_cached_mask(causal):
+    rng = np.random.default_rng(21)
+    code, h, kvh, d, bs, nb = orc.BF16, 8, 4, 64, 16, 64
+    prior, qlens = [0, 19, 40], [23, 9, 1]
+    q, kc, vc, bt, lens, cu = _prefill_case(rng, code, h, kvh, d, bs, prior, qlens, nb)
+    scale = d ** -0.5
+    got = orc.prefill_attention(q, kc, vc, bt, lens, cu, scale, causal=causal, dtype=code)
+    for s in range(len(lens)):
+        L, n, P = int(lens[s]), qlens[s], prior[s]
+        ki, vi = inverse_layout(kc, vc, bt[s, :(L + bs - 1) // bs], L)
+        K = torch.from_numpy(orc.to_f32(ki, code).astype(np.float64)).repeat_interleave(2, 0)
+        V = torch.from_numpy(orc.to_f32(vi, code).astype(np.float64)).repeat_interleave(2, 0)
+        Q = torch.from_numpy(orc.to_f32(q[cu[s]:cu[s + 1]], code).astype(np.float64)).transpose(0, 1)
+        if causal:
+            # make_causal_mask_cached: key kv allowed for query i iff kv <= P + i
+            mask = torch.from_numpy(np.tril(np.ones((n, L), dtype=bool), k=P))
+        else:
+            mask = torch.ones((n, L), dtype=torch.bool)
+        want = torch.nn.functional.scaled_dot_product_attention(Q, K, V, attn_mask=mask, scale=scale)
+        logits = (Q @ K.transpose(1, 2)) * scale
+        logits = logits.masked_fill(~mask, float("-inf"))
+        m = logits.max(dim=-1, keepdim=True).values
+        S = torch.exp(torch.logsumexp(logits, dim=-1, keepdim=True) - m)
+        g = torch.from_numpy(got[cu[s]:cu[s + 1]]).transpose(0, 1)
+        torch.testing.assert_close(g * (S + 1e-6) / S, want, rtol=1e-10, atol=1e-12)
+    if prior[0] == 0 and causal:
+        # P = 0 reduces to plain causal attention
+        L = qlens[0]
+        ki, vi = inverse_layout(kc, vc, bt[0, :(L + bs - 1) // bs], L)
+        K = torch.from_numpy(orc.to_f32(ki, code).astype(np.float64)).repeat_interleave(2, 0)
+        V = torch.from_numpy(orc.to_f32(vi, code).astype(np.float64)).repeat_interleave(2, 0)
+        Q = torch.from_numpy(orc.to_f32(q[:L], code).astype(np.float64)).transpose(0, 1)
+        want = torch.nn.functional.scaled_dot_product_attention(Q, K, V, is_causal=True, scale=scale)
+        g = torch.from_numpy(got[:L]).transpose(0, 1)
+        torch.testing.assert_close(g, want, rtol=2e-6, atol=1e-9)
+
+
+def test_prefill_cached_causal_mask_kat():
+    """attention.rs:870-909: cache_len=3, new_len=2 -> query 0 (abs 3) sees
+    keys 0..3, query 1 (abs 4) sees all 5. Keys are zero so visible keys get
+    equal weight; one-hot values reveal which keys were seen."""
+    code, h, kvh, d, bs = orc.F32, 1, 1, 64, 8
+    nb = 2
+    kc = np.zeros((nb, kvh, d // 4, bs, 4), dtype=np.float32)
+    vc = np.zeros((nb, kvh, d, bs), dtype=np.float32)
+    for t in range(5):
+        vc[1, 0, t, t] = 1.0          # token t lives in block 1 offset t; V_t = e_t
+    bt = np.array([[1]], dtype=np.uint32)
+    q = np.ones((2, h, d), dtype=np.float32)
+    out = orc.prefill_attention(q, kc, vc, bt, np.array([5], dtype=np.uint32),
+                                np.array([0, 2], dtype=np.uint32), 1.0, causal=True, dtype=code)
+    np.testing.assert_allclose(out[0, 0, :5], np.array([1, 1, 1, 1, 0]) / (4 + 1e-6), rtol=1e-12)
+    np.testing.assert_allclose(out[1, 0, :5], np.ones(5) / (5 + 1e-6), rtol=1e-12)
+
+
+def test_prefill_matches_reference_packed_vs_unpacked_kat():
+    """attention.rs:949-1041: batch 2, seq 4, head_dim 32, 2 q heads / 1 kv
+    head, query_lens = kv_lens = [3, 2], q = i*0.01, kv = i*0.02 + 1 (K = V),
+    causal, checked against per-sequence matmul/softmax/matmul at 1e-4."""
+    d, h, kvh, bs = 32, 2, 1, 4
+    qfull = (np.arange(2 * h * 4 * d, dtype=np.float32) * 0.01).reshape(2, h, 4, d)
+    qlens = [3, 2]
+    packed = (np.arange(5 * kvh * d, dtype=np.float32) * 0.02 + 1.0).reshape(5, kvh, d)
+    nb = 4
+    kc = np.zeros((nb, kvh, d // 4, bs, 4), dtype=np.float32)
+    vc = np.zeros((nb, kvh, d, bs), dtype=np.float32)
+    bt = np.array([[2], [3]], dtype=np.uint32)
+    slots = np.array([8, 9, 10, 12, 13], dtype=np.int64)
+    orc.reshape_and_cache(packed, packed.copy(), kc, vc, slots, dtype=orc.F32)
+    q = np.ascontiguousarray(np.concatenate([qfull[0, :, :3].transpose(1, 0, 2),
+                                             qfull[1, :, :2].transpose(1, 0, 2)]))
+    out = orc.prefill_attention(q, kc, vc, bt, np.array([3, 2], dtype=np.uint32),
+                                np.array([0, 3, 5], dtype=np.uint32), d ** -0.5, causal=True,
+                                dtype=orc.F32)
+    start = 0
+    for s, n in enumerate(qlens):
+        kv = torch.from_numpy(packed[start:start + n].transpose(1, 0, 2)).repeat_interleave(2, 0)
+        qr = torch.from_numpy(qfull[s, :, :n])
+        w = qr @ kv.transpose(1, 2) * d ** -0.5
+        w = w + torch.triu(torch.full((n, n), float("-inf")), 1)
+        ref = torch.softmax(w, dim=-1) @ kv
+        got = torch.from_numpy(out[start:start + n]).transpose(0, 1).float()
+        assert (got - ref).abs().max().item() <= 1e-4
+        start += n
+
+
+def test_cpu_baseline_matches_oracle():
+    rng = np.random.default_rng(11)
+    code, h, kvh, d, bs, nb = orc.BF16, 16, 8, 128, 16, 64
+    lens = np.array([100, 5, 260], dtype=np.uint32)
+    q, kc, vc, bt = _random_decode(rng, code, 3, h, kvh, d, bs, lens, nb)
+    nk = orc.from_f32(rng.standard_normal((3, kvh, d)).astype(np.float32), code)
+    nv = orc.from_f32(rng.standard_normal((3, kvh, d)).astype(np.float32), code)
+    pos = lens.astype(np.int64) - 1
+    slots = bt[np.arange(3), pos // bs].astype(np.int64) * bs + pos % bs
+    kc2, vc2 = kc.copy(), vc.copy()
+    out, threads = orc.cpu_baseline_decode_step(q, nk, nv, slots, kc2, vc2, bt, lens, d ** -0.5,
+                                                dtype=code)
+    assert threads >= 1
+    orc.reshape_and_cache(nk, nv, kc, vc, slots, dtype=code)
+    np.testing.assert_array_equal(kc, kc2)
+    want = orc.paged_attention(q, kc, vc, bt, lens, int(lens.max()), d ** -0.5, dtype=code)
+    np.testing.assert_allclose(out, want, rtol=1e-4, atol=1e-5)
