@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <atomic>
 #include <string>
 
 #include "vpa_internal.h"
@@ -14,6 +16,7 @@ namespace vpa {
 
 namespace {
 thread_local std::string g_last_error;
+constexpr int kMaxDevices = 64;
 }
 
 int fail(int code, const char* fmt, ...) {
@@ -96,6 +99,23 @@ int check_cache(const char* op, int32_t cache_dtype, int32_t num_kv_heads, int32
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: caches must be 16-byte aligned", op);
   return VPA_OK;
 }
+
+}  // namespace
+
+int device_cu_count() {
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0)
+    n = 256;
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+namespace {
 
 int hip_status(const char* op, hipError_t e) {
   if (e == hipSuccess) return VPA_OK;
@@ -231,12 +251,23 @@ int vpa_paged_attention(void* out, const void* query, const float* k_scale,
   if (!decode_supported(dtype, head_dim, block_size, group))
     return fail(VPA_ERR_UNSUPPORTED,
                 "%s: no kernel for %d query heads per kv head (supported: 1, 2, 4)", op, group);
-  if (max_context_len > kDecodeMaxPartitions * kDecodePartitionTokens)
+  if (max_context_len > kDecodeMaxPartitions * kDecodeMinPartitionTokens)
     return fail(VPA_ERR_UNSUPPORTED, "%s: max_context_len=%d exceeds %d", op, max_context_len,
-                kDecodeMaxPartitions * kDecodePartitionTokens);
+                kDecodeMaxPartitions * kDecodeMinPartitionTokens);
   if (num_seqs == 0) return VPA_OK;
   if (num_seqs > 65535)
     return fail(VPA_ERR_UNSUPPORTED, "%s: num_seqs=%d exceeds 65535", op, num_seqs);
+  {
+    // one wavefront per (sequence, partition, kv head): keep the 1-D grid
+    // below 2^25 workgroups
+    const int64_t parts =
+        std::max<int64_t>(1, ((int64_t)max_context_len + kDecodeMinPartitionTokens - 1) /
+                                 kDecodeMinPartitionTokens);
+    if ((int64_t)num_seqs * parts * num_kv_heads > ((int64_t)1 << 25))
+      return fail(VPA_ERR_UNSUPPORTED,
+                  "%s: num_seqs * ceil(max_context_len/%d) * num_kv_heads exceeds 2^25", op,
+                  kDecodeMinPartitionTokens);
+  }
   if (out == nullptr || query == nullptr || block_tables == nullptr || context_lens == nullptr)
     return fail(VPA_ERR_INVALID_ARGUMENT,
                 "%s: out, query, block_tables and context_lens must be non-null", op);

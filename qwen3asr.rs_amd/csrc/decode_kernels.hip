@@ -25,6 +25,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 #include "vpa_device.h"
 #include "vpa_internal.h"
 
@@ -258,25 +260,387 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
   }
 }
 
-// One wave per (query head, sequence) with more than one partition.
+// ---------------------------------------------------------------------------
+// Fast decode path for 16-bit caches with head_dim <= 128 (x = 8, at most 16
+// chunks per key row).
+//
+// Work list: decode_plan_kernel (one workgroup) turns context_lens into the
+// list of (sequence, partition) items of PT tokens, resets the work queue and
+// the per-(sequence, kv head) completion counters. All of it lives in the
+// caller's workspace and is rebuilt by every call, so the pair of launches
+// can be captured in a graph and replayed with new lengths.
+//
+// paged_decode_rows_kernel: persistent wavefronts take (item, kv head) work
+// units from the queue with one atomic per unit, so no workgroup is spent on
+// partitions past a sequence's end and short and long sequences balance
+// automatically. Per unit, with no cross-lane reduction in the loops:
+//   K pass: 64 / BS blocks per iteration, lane l owns token l % BS of block
+//     l / BS and loads its whole key row (the D/8 chunks at stride BS*16 B;
+//     16 lanes x 16 B = 256 B contiguous per chunk and block). q of the G
+//     heads is staged in LDS and read as broadcasts. Logits go to LDS.
+//   softmax: DPP max / sum over the partition; probabilities are stored in
+//     LDS rounded to the cache type.
+//   V pass: each load instruction reads 1 KiB contiguous of a value tile;
+//     lane l owns rows l / (BS/8) + k * 64 / (BS/8) over 8 tokens, and the
+//     BS/8 lanes of a row are summed with DPP once at the end.
+// A sequence with several partitions writes f32 partials, merged by
+// decode_merge_kernel over the plan's list of multi-partition sequences.
+// (Merging in the last wave to finish would need an agent-scope release per
+// partition, which on gfx950 writes back the whole L2: far more expensive
+// than one extra launch.)
+// ---------------------------------------------------------------------------
+// Floats per split-K partial row of the rows path: D outputs + a 32-float
+// line holding {max, sum}.
+template <int D>
+constexpr int kPartRow = D + 32;
+
+__device__ __forceinline__ int clamp_context(uint32_t ctx, int max_ctx, int cap) {
+  return min((int)min(ctx, (uint32_t)max_ctx), cap);
+}
+
+__global__ __launch_bounds__(1024) void decode_plan_kernel(
+    const uint32_t* __restrict__ context_lens, int32_t num_seqs, int32_t max_ctx,
+    int32_t cap_tokens, int32_t part_tokens, uint2* __restrict__ items,
+    uint32_t* __restrict__ multi, uint32_t* __restrict__ queue) {
+  __shared__ uint32_t s_sum[1024];
+  __shared__ uint32_t s_multi;
+  if (threadIdx.x == 0) s_multi = 0;
+  const int tid = threadIdx.x;
+  const int chunk = (num_seqs + 1023) / 1024;
+  const int s0 = min(tid * chunk, num_seqs);
+  const int s1 = min(s0 + chunk, num_seqs);
+  uint32_t local = 0;
+  for (int s = s0; s < s1; ++s) {
+    const int L = clamp_context(context_lens[s], max_ctx, cap_tokens);
+    local += L > 0 ? (uint32_t)((L + part_tokens - 1) / part_tokens) : 1u;
+  }
+  s_sum[tid] = local;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const uint32_t v = tid >= off ? s_sum[tid - off] : 0u;
+    __syncthreads();
+    s_sum[tid] += v;
+    __syncthreads();
+  }
+  uint32_t pos = s_sum[tid] - local;
+  for (int s = s0; s < s1; ++s) {
+    const int L = clamp_context(context_lens[s], max_ctx, cap_tokens);
+    const int n = L > 0 ? (L + part_tokens - 1) / part_tokens : 1;
+    for (int p = 0; p < n; ++p)
+      items[pos++] = make_uint2(((uint32_t)s << 16) | (uint32_t)p, (uint32_t)max(L, 0));
+    if (n > 1) multi[atomicAdd(&s_multi, 1u)] = (uint32_t)s;
+  }
+  __syncthreads();
+  if (tid == 1023) {
+    queue[0] = 0u;
+    queue[1] = s_sum[1023];
+    queue[2] = s_multi;
+  }
+}
+
+#ifndef VPA_DECODE_ROWS_WAVES_PER_EU
+#define VPA_DECODE_ROWS_WAVES_PER_EU 3
+#endif
+
+// Workgroup of NW waves = one (sequence, kv head, chunk of NW * PT tokens)
+// work unit. Wave w attends over partition w of the chunk (PT tokens); the NW
+// partial results are merged in LDS, so HBM partial rows are only written for
+// sequences longer than one chunk.
+template <typename T, int D, int BS, int G, int PT, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(VPA_DECODE_ROWS_WAVES_PER_EU)))
+void paged_decode_rows_kernel(
+    T* __restrict__ out, const T* __restrict__ query, const T* __restrict__ key_cache,
+    const T* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
+    int32_t block_table_stride, float scale, int32_t num_heads, int32_t num_kv_heads,
+    int64_t num_blocks, int64_t block_stride, int64_t head_stride, float* __restrict__ part_out,
+    int32_t max_parts, const uint2* __restrict__ items, const uint32_t* __restrict__ queue) {
+  constexpr int X = pack_x<T>();
+  static_assert(X == 8, "16-bit element types only");
+  constexpr int PB = PT / BS;        // blocks per wave partition
+  constexpr int VPR = BS / X;        // 16-byte vectors per value row
+  constexpr int NVV = D * VPR / 64;  // value vectors per lane per block
+  constexpr int DSTEP = 64 / VPR;    // row stride between a lane's value vectors
+  constexpr int NPL = PT / 64;       // partition tokens per lane in the softmax
+  // Stages of NV = 8 loads per lane (8 KiB per wave). A K stage reads BKS
+  // key tiles: load k of a tile gives lane l vector l + 64k, i.e. token
+  // l % BS and 16-byte chunk l / BS + k * (64 / BS), so each instruction
+  // reads 1 KiB contiguous and the lane needs only those chunks of q
+  // (held in registers); the partial dot products of a token are summed
+  // over its 64 / BS lanes with DPP / permlane swaps. A V stage reads BKS
+  // value tiles the same way (lane l: row l / (BS/8) + k * 64 / (BS/8),
+  // tokens (l % (BS/8)) * 8 .. +7).
+  constexpr int NV = 8;                   // 16-byte loads per lane per stage
+  constexpr int KPL = D * BS / (X * 64);  // loads per lane per tile (K or V)
+  constexpr int LPT = 64 / BS;            // lanes per token in a key tile
+  constexpr int BKS = NV / KPL;           // tiles per stage
+  static_assert(KPL == NVV && KPL >= 1 && KPL <= NV && NV % KPL == 0, "stage shape");
+  static_assert(VPR >= 1 && VPR <= 4 && PB <= 64 && PT % 64 == 0 && PT >= D, "shape");
+
+  __shared__ float s_logit[NW][G][PT];
+  __shared__ __align__(16) uint16_t s_p[NW][G][PT];
+  __shared__ float s_m[NW][G], s_l[NW][G];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const uint32_t w = blockIdx.x;
+  if (w >= queue[1] * (uint32_t)num_kv_heads) return;  // surplus workgroup of the grid
+  const uint2 item = items[w / (uint32_t)num_kv_heads];
+  const int j = (int)(w % (uint32_t)num_kv_heads);
+  const int s = (int)(item.x >> 16);
+  const int chunk = (int)(item.x & 0xffffu);
+  const int L = (int)item.y;
+  if (L <= 0) {
+    for (int i = threadIdx.x; i < G * D; i += 64 * NW)
+      store_from_f32<T>(out + ((int64_t)s * num_heads + j * G) * D + i, 0.f);
+    return;
+  }
+  const int nblk = (L + BS - 1) / BS;
+  const int nchunks = (nblk + PB * NW - 1) / (PB * NW);
+  const int b_begin = (chunk * NW + wave) * PB;
+  const int nb = min(PB, nblk - b_begin);  // <= 0: this wave's partition is past the end
+
+  float acc[G][NVV];
+  float m[G], lsum[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    lsum[g] = 0.f;
+#pragma unroll
+    for (int k = 0; k < NVV; ++k) acc[g][k] = 0.f;
+  }
+
+  if (nb > 0) {
+    // block ids of the partition (lane b holds block b) and this lane's q chunks
+    const uint32_t my_bt =
+        lane < nb ? block_tables[(int64_t)s * block_table_stride + b_begin + lane] : 0u;
+    uint4 qv[G][KPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const T* qrow = query + ((int64_t)s * num_heads + j * G + g) * D;
+#pragma unroll
+      for (int k = 0; k < KPL; ++k)
+        qv[g][k] = *reinterpret_cast<const uint4*>(qrow + (lane / BS + k * LPT) * X);
+    }
+
+    const int64_t head_off = (int64_t)j * head_stride;
+    const uint4* kbase = reinterpret_cast<const uint4*>(key_cache + head_off);
+    const uint4* vbase = reinterpret_cast<const uint4*>(value_cache + head_off);
+    const int64_t bstride_v = block_stride / X;
+    const int t = lane % BS;     // K: token of this lane within a tile
+    const int seg = lane % VPR;  // V: 8-token segment of this lane
+    const int nks = (((nb + BKS - 1) / BKS) + 1) & ~1;  // stages per pass, rounded up to even
+    float* const my_logit = &s_logit[wave][0][0];
+    uint16_t* const my_p = &s_p[wave][0][0];
+
+    // Block id of tile u of stage st (uniform); blocks past the partition
+    // or out of the pool read block 0 (in bounds) and are masked when
+    // consumed, so loads never branch.
+    auto tile_block = [&](int st, int u, bool& ok) -> uint32_t {
+      const int bi = st * BKS + u;
+      const uint32_t phys = (uint32_t)__builtin_amdgcn_readlane((int)my_bt, bi < nb ? bi : 0);
+      ok = bi < nb && (int64_t)phys < num_blocks;
+      return ok ? phys : 0u;
+    };
+    auto load_stage = [&](const uint4* base, int st, uint4(&buf)[NV]) {
+#pragma unroll
+      for (int u = 0; u < BKS; ++u) {
+        bool ok;
+        const uint4* tp = base + (int64_t)tile_block(st, u, ok) * bstride_v + lane;
+#pragma unroll
+        for (int k = 0; k < KPL; ++k) buf[u * KPL + k] = tp[64 * k];
+      }
+    };
+    // logits of BKS tiles
+    auto compute_k = [&](int st, const uint4(&buf)[NV]) {
+#pragma unroll
+      for (int u = 0; u < BKS; ++u) {
+        bool ok;
+        tile_block(st, u, ok);
+        const int bi = st * BKS + u;
+        const bool valid = ok && (b_begin + bi) * BS + t < L;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float qk = 0.f;
+#pragma unroll
+          for (int k = 0; k < KPL; ++k) qk = dot16<T>(qv[g][k], buf[u * KPL + k], qk);
+          qk = sum_lanes_mod<BS>(qk);
+          if (lane < BS && bi < PB) my_logit[g * PT + bi * BS + lane] = valid ? qk * scale : -INFINITY;
+        }
+      }
+    };
+    // P.V over BKS tiles
+    auto compute_v = [&](int st, const uint4(&buf)[NV]) {
+#pragma unroll
+      for (int u = 0; u < BKS; ++u) {
+        bool ok;
+        tile_block(st, u, ok);
+        if (!ok) continue;
+        const int bi = st * BKS + u;
+        uint4 vv[NVV];
+#pragma unroll
+        for (int k = 0; k < NVV; ++k) vv[k] = buf[u * KPL + k];
+        const int tok0 = (b_begin + bi) * BS + seg * X;
+        if (tok0 + X > L) {
+          // past the context in the last block: zero the values (stale contents)
+#pragma unroll
+          for (int k = 0; k < NVV; ++k) {
+            union {
+              uint4 v;
+              uint16_t e[X];
+            } wv;
+            wv.v = vv[k];
+#pragma unroll
+            for (int e = 0; e < X; ++e)
+              if (tok0 + e >= L) wv.e[e] = 0;
+            vv[k] = wv.v;
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const uint4 pk = *reinterpret_cast<const uint4*>(&my_p[g * PT + bi * BS + seg * X]);
+#pragma unroll
+          for (int k = 0; k < NVV; ++k) acc[g][k] = dot16<T>(pk, vv[k], acc[g][k]);
+        }
+      }
+    };
+
+    // ---- software pipeline (nks even): the next stage's loads are in
+    // flight while the current stage is computed; the first two V stages are
+    // issued during the last two K stages, before the softmax ----
+    uint4 bufA[NV], bufB[NV];
+    load_stage(kbase, 0, bufA);
+    load_stage(kbase, 1, bufB);
+    for (int st = 0; st + 2 < nks; st += 2) {
+      compute_k(st, bufA);
+      load_stage(kbase, st + 2, bufA);
+      compute_k(st + 1, bufB);
+      load_stage(kbase, st + 3, bufB);
+    }
+    compute_k(nks - 2, bufA);
+    load_stage(vbase, 0, bufA);
+    compute_k(nks - 1, bufB);
+    load_stage(vbase, 1, bufB);
+
+    // ---- softmax over the partition ----
+    lds_wave_sync();
+    {
+      const int ntok = nb * BS;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float v[NPL];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+          const int idx = i * 64 + lane;
+          v[i] = idx < ntok ? my_logit[g * PT + idx] : -INFINITY;
+          mx = fmaxf(mx, v[i]);
+        }
+        mx = wave_max_dpp(mx);
+        float sm = 0.f;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+          const float p = v[i] == -INFINITY ? 0.f : expf(v[i] - mx);
+          sm += p;
+          T pt;
+          store_from_f32<T>(&pt, p);
+          my_p[g * PT + i * 64 + lane] = pt.x;
+        }
+        m[g] = mx;
+        lsum[g] = wave_sum_dpp(sm);
+      }
+    }
+    lds_wave_sync();
+
+    for (int st = 0; st + 2 < nks; st += 2) {
+      compute_v(st, bufA);
+      load_stage(vbase, st + 2, bufA);
+      compute_v(st + 1, bufB);
+      load_stage(vbase, st + 3, bufB);
+    }
+    compute_v(nks - 2, bufA);
+    compute_v(nks - 1, bufB);
+
+    // sum the VPR lanes that hold the same value row
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < NVV; ++k) {
+        if constexpr (VPR >= 2) acc[g][k] += dpp<kDppQuadXor1>(acc[g][k]);
+        if constexpr (VPR >= 4) acc[g][k] += dpp<kDppQuadXor2>(acc[g][k]);
+      }
+  }
+
+  // ---- merge the NW partitions of the chunk in LDS ----
+  // Each wave leaves its unnormalised output (in its own s_logit slot, free
+  // after the softmax) and its max / sum; then the workgroup combines them.
+  __syncthreads();
+  {
+    float* my_row = &s_logit[wave][0][0];
+    const int row0 = lane / VPR;
+    if (lane % VPR == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < NVV; ++k) my_row[g * D + row0 + k * DSTEP] = acc[g][k];
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = lsum[g];
+      }
+    }
+  }
+  __syncthreads();
+  // thread e of the workgroup combines output elements e, e + 64*NW, ...
+  // (contiguous per head row, so stores write whole lines)
+  const bool single = nchunks == 1;
+  for (int e = threadIdx.x; e < G * D; e += 64 * NW) {
+    const int g = e / D, d = e - (e / D) * D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) mx = fmaxf(mx, s_m[q][g]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      const float wq = s_m[q][g] == -INFINITY ? 0.f : expf(s_m[q][g] - mx);
+      num = fmaf(wq, s_logit[q][0][g * D + d], num);
+      den = fmaf(wq, s_l[q][g], den);
+    }
+    const int h = j * G + g;
+    if (single) {
+      store_from_f32<T>(out + ((int64_t)s * num_heads + h) * D + d, num / (den + 1e-6f));
+    } else {
+      // split-K partial row: D floats of unnormalised output, then one
+      // 128-byte line {max, sum, 0...} (whole lines: partial-line stores
+      // cost a read-modify-write in HBM)
+      float* prow = part_out + (((int64_t)s * num_heads + h) * max_parts + chunk) * kPartRow<D>;
+      prow[d] = num;
+      if (d < 32) prow[D + d] = d == 0 ? mx : (d == 1 ? den : 0.f);
+    }
+  }
+}
+
+// One wave per (query head, sequence) with more than one partition: merge of
+// the generic kernel's split-K partials.
 template <typename T, int D>
 __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
     T* __restrict__ out, const uint32_t* __restrict__ context_lens, int32_t max_ctx,
     int32_t block_table_stride, int32_t block_size, int32_t num_heads,
     const float* __restrict__ part_out, const float* __restrict__ part_max,
-    const float* __restrict__ part_sum, int32_t max_parts) {
+    const float* __restrict__ part_sum, int32_t max_parts, int32_t part_tokens) {
   __shared__ float s_w[kDecodeMaxPartitions];
   const int lane = threadIdx.x;
   const int h = blockIdx.x;
   const int s = blockIdx.y;
   const int L = min((int)min(context_lens[s], (uint32_t)max_ctx), block_table_stride * block_size);
-  const int nparts = (L + kPT - 1) / kPT;
+  const int nparts = (L + part_tokens - 1) / part_tokens;
   if (nparts <= 1) return;
 
   const int64_t row0 = ((int64_t)s * num_heads + h) * max_parts;
   float mx = -INFINITY;
   for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, part_max[row0 + p]);
-  mx = wave_max_range<1, 32>(mx);
+  mx = wave_max_dpp(mx);
   float tot = 0.f;
   for (int p = lane; p < nparts; p += 64) {
     const float pm = part_max[row0 + p];
@@ -284,7 +648,7 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
     s_w[p] = w;
     tot += w * part_sum[row0 + p];
   }
-  tot = wave_sum_range<1, 32>(tot);
+  tot = wave_sum_dpp(tot);
   lds_wave_sync();
   const float inv = 1.f / (tot + 1e-6f);
   T* orow = out + ((int64_t)s * num_heads + h) * D;
@@ -293,6 +657,110 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
     for (int p = 0; p < nparts; ++p) a = fmaf(s_w[p], part_out[(row0 + p) * D + d], a);
     store_from_f32<T>(orow + d, a * inv);
   }
+}
+
+#ifndef VPA_DECODE_ROWS_PT
+#define VPA_DECODE_ROWS_PT 128
+#endif
+#ifndef VPA_DECODE_ROWS_WAVES
+#define VPA_DECODE_ROWS_WAVES 4
+#endif
+constexpr int kRowsPT = VPA_DECODE_ROWS_PT;  // partition tokens per wave of the rows kernel
+constexpr int kRowsWaves = VPA_DECODE_ROWS_WAVES;  // waves (partitions) per workgroup
+static_assert(kRowsPT >= kDecodeMinPartitionTokens, "workspace sized for 128-token partitions");
+
+// Merge of split-K partials: persistent waves over (multi-partition
+// sequence from the plan, query head) units.
+template <typename T, int D>
+__global__ __launch_bounds__(64) void decode_merge_kernel(
+    T* __restrict__ out, const uint32_t* __restrict__ context_lens, int32_t max_ctx,
+    int32_t cap_tokens, int32_t part_tokens, int32_t num_heads, const float* __restrict__ part,
+    int32_t max_parts, const uint32_t* __restrict__ multi, const uint32_t* __restrict__ queue) {
+  constexpr int DPL = D / 64;
+  constexpr int RS = kPartRow<D>;
+  __shared__ float s_w[64];
+  const int lane = threadIdx.x;
+  const uint32_t units = queue[2] * (uint32_t)num_heads;
+  for (uint32_t u = blockIdx.x; u < units; u += gridDim.x) {
+    const int s = (int)multi[u / (uint32_t)num_heads];
+    const int h = (int)(u % (uint32_t)num_heads);
+    const int L = clamp_context(context_lens[s], max_ctx, cap_tokens);
+    const int nparts = (L + part_tokens - 1) / part_tokens;
+    const float* rows = part + ((int64_t)s * num_heads + h) * max_parts * RS;
+    float mx = -INFINITY;
+    for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, rows[(int64_t)p * RS + D]);
+    mx = wave_max_dpp(mx);
+    float tot = 0.f;
+    float a[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) a[k] = 0.f;
+    for (int c0 = 0; c0 < nparts; c0 += 64) {
+      const int p = c0 + lane;
+      float wgt = 0.f;
+      if (p < nparts) {
+        const float pm = rows[(int64_t)p * RS + D];
+        wgt = pm == -INFINITY ? 0.f : expf(pm - mx);
+        tot += wgt * rows[(int64_t)p * RS + D + 1];
+      }
+      lds_wave_sync();
+      s_w[lane] = wgt;
+      lds_wave_sync();
+      const int cn = min(64, nparts - c0);
+      int q = 0;
+      // four partial rows in flight per step
+      for (; q + 4 <= cn; q += 4) {
+        float v[4][DPL];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) v[r][k] = rows[(int64_t)(c0 + q + r) * RS + lane + 64 * k];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) a[k] = fmaf(s_w[q + r], v[r][k], a[k]);
+      }
+      for (; q < cn; ++q) {
+#pragma unroll
+        for (int k = 0; k < DPL; ++k)
+          a[k] = fmaf(s_w[q], rows[(int64_t)(c0 + q) * RS + lane + 64 * k], a[k]);
+      }
+    }
+    tot = wave_sum_dpp(tot);
+    const float inv = 1.f / (tot + 1e-6f);
+    T* orow = out + ((int64_t)s * num_heads + h) * D + lane;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) store_from_f32<T>(orow + 64 * k, a[k] * inv);
+    lds_wave_sync();
+  }
+}
+
+template <typename T, int D, int BS, int G>
+hipError_t launch_decode_rows(void* out, const void* q, const void* kc, const void* vc,
+                              const uint32_t* bt, int32_t bts, const uint32_t* cl,
+                              int32_t max_ctx, float scale, int32_t num_seqs, int32_t num_heads,
+                              const CacheGeom& g, const DecodeWorkspace& ws, hipStream_t stream) {
+  constexpr int kChunk = kRowsPT * kRowsWaves;  // tokens per workgroup
+  const int cap_tokens = bts * g.block_size;
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, cl, num_seqs, max_ctx,
+                     cap_tokens, kChunk, ws.items, ws.multi, ws.queue);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int max_chunks = max(1, (max_ctx + kChunk - 1) / kChunk);
+  const int64_t units = (int64_t)num_seqs * max_chunks * g.num_kv_heads;
+  hipLaunchKernelGGL((paged_decode_rows_kernel<T, D, BS, G, kRowsPT, kRowsWaves>),
+                     dim3((unsigned)units), dim3(64 * kRowsWaves), 0, stream,
+                     static_cast<T*>(out), static_cast<const T*>(q), static_cast<const T*>(kc),
+                     static_cast<const T*>(vc), bt, bts, scale, num_heads, g.num_kv_heads,
+                     g.num_blocks, g.block_stride, g.head_stride, ws.part_out, ws.max_parts,
+                     ws.items, ws.queue);
+  e = hipGetLastError();
+  if (e != hipSuccess || max_chunks <= 1) return e;
+  const int64_t munits = (int64_t)num_seqs * num_heads;
+  const int64_t mwaves = std::min<int64_t>(munits, (int64_t)device_cu_count() * 8);
+  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)mwaves), dim3(64), 0, stream,
+                     static_cast<T*>(out), cl, max_ctx, cap_tokens, kChunk, num_heads,
+                     ws.part_out, ws.max_parts, ws.multi, ws.queue);
+  return hipGetLastError();
 }
 
 template <typename T, int D, int BS, int G>
@@ -312,7 +780,7 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   dim3 rgrid((unsigned)num_heads, (unsigned)num_seqs);
   hipLaunchKernelGGL((paged_decode_reduce_kernel<T, D>), rgrid, dim3(64), 0, stream,
                      static_cast<T*>(out), cl, max_ctx, bts, g.block_size, num_heads, ws.part_out,
-                     ws.part_max, ws.part_sum, ws.max_parts);
+                     ws.part_max, ws.part_sum, ws.max_parts, kPT);
   return hipGetLastError();
 }
 
@@ -320,6 +788,24 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (group == 1) return launch_decode_t<T, D, BS, 1>(args...);         \
   if (group == 2) return launch_decode_t<T, D, BS, 2>(args...);         \
   if (group == 4) return launch_decode_t<T, D, BS, 4>(args...);
+
+#define VPA_DECODE_ROWS_G(T, D, BS)                                  \
+  if (group == 1) return launch_decode_rows<T, D, BS, 1>(args...);   \
+  if (group == 2) return launch_decode_rows<T, D, BS, 2>(args...);   \
+  if (group == 4) return launch_decode_rows<T, D, BS, 4>(args...);
+
+// 16-bit caches with head_dim <= 128 use the rows kernel; f32 and
+// head_dim 256 use the generic kernel.
+#define VPA_DECODE_DBS16(T)                                   \
+  if (D == 64 && BS == 8) { VPA_DECODE_ROWS_G(T, 64, 8) }     \
+  if (D == 64 && BS == 16) { VPA_DECODE_ROWS_G(T, 64, 16) }   \
+  if (D == 64 && BS == 32) { VPA_DECODE_ROWS_G(T, 64, 32) }   \
+  if (D == 128 && BS == 8) { VPA_DECODE_ROWS_G(T, 128, 8) }   \
+  if (D == 128 && BS == 16) { VPA_DECODE_ROWS_G(T, 128, 16) } \
+  if (D == 128 && BS == 32) { VPA_DECODE_ROWS_G(T, 128, 32) } \
+  if (D == 256 && BS == 8) { VPA_DECODE_G(T, 256, 8) }        \
+  if (D == 256 && BS == 16) { VPA_DECODE_G(T, 256, 16) }      \
+  if (D == 256 && BS == 32) { VPA_DECODE_G(T, 256, 32) }
 
 #define VPA_DECODE_DBS(T)                                   \
   if (D == 64 && BS == 8) { VPA_DECODE_G(T, 64, 8) }        \
@@ -334,8 +820,8 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
 
 template <typename... A>
 hipError_t dispatch_decode(int dtype, int D, int BS, int group, A... args) {
-  if (dtype == VPA_DTYPE_BF16) { VPA_DECODE_DBS(bf16_t) }
-  if (dtype == VPA_DTYPE_F16) { VPA_DECODE_DBS(f16_t) }
+  if (dtype == VPA_DTYPE_BF16) { VPA_DECODE_DBS16(bf16_t) }
+  if (dtype == VPA_DTYPE_F16) { VPA_DECODE_DBS16(f16_t) }
   if (dtype == VPA_DTYPE_F32) { VPA_DECODE_DBS(float) }
   return hipErrorInvalidValue;
 }
@@ -347,27 +833,49 @@ bool decode_supported(int dtype, int head_dim, int block_size, int group) {
          (group == 1 || group == 2 || group == 4);
 }
 
-size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len) {
-  const int max_parts = (max_context_len + kPT - 1) / kPT;
-  if (max_parts <= 1 || num_seqs <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
-  const size_t rows = (size_t)num_seqs * (size_t)num_heads * (size_t)max_parts;
+namespace {
+struct WorkspacePlan {
+  size_t part_out, part_stat, items, multi, queue, total;
+  int max_parts;
+};
+WorkspacePlan plan_workspace(int num_seqs, int num_heads, int head_dim, int max_context_len) {
   auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
-  return up(rows * (size_t)head_dim * sizeof(float)) + 2 * up(rows * sizeof(float));
+  constexpr int kMin = kDecodeMinPartitionTokens;
+  WorkspacePlan w{};
+  w.max_parts = (max_context_len + kMin - 1) / kMin;
+  const size_t rows = w.max_parts > 1 ? (size_t)num_seqs * (size_t)num_heads * (size_t)w.max_parts : 0;
+  w.part_out = up(rows * (size_t)(head_dim + 32) * sizeof(float));
+  w.part_stat = up(rows * sizeof(float));
+  w.items = up((size_t)num_seqs * (size_t)(w.max_parts > 1 ? w.max_parts : 1) * sizeof(uint2));
+  w.multi = up((size_t)num_seqs * sizeof(uint32_t));
+  w.queue = 256;
+  w.total = w.part_out + 2 * w.part_stat + w.items + w.multi + w.queue;
+  return w;
+}
+}  // namespace
+
+size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len) {
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_context_len < 0) return 0;
+  return plan_workspace(num_seqs, num_heads, head_dim, max_context_len).total;
 }
 
 DecodeWorkspace carve_decode_workspace(void* base, int num_seqs, int num_heads, int head_dim,
                                        int max_context_len) {
   DecodeWorkspace ws{};
-  ws.max_parts = (max_context_len + kPT - 1) / kPT;
-  if (ws.max_parts <= 1) return ws;
-  const size_t rows = (size_t)num_seqs * (size_t)num_heads * (size_t)ws.max_parts;
-  auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const WorkspacePlan w = plan_workspace(num_seqs, num_heads, head_dim, max_context_len);
+  ws.max_parts = w.max_parts;
   char* p = static_cast<char*>(base);
   ws.part_out = reinterpret_cast<float*>(p);
-  p += up(rows * (size_t)head_dim * sizeof(float));
+  p += w.part_out;
   ws.part_max = reinterpret_cast<float*>(p);
-  p += up(rows * sizeof(float));
+  p += w.part_stat;
   ws.part_sum = reinterpret_cast<float*>(p);
+  p += w.part_stat;
+  ws.items = reinterpret_cast<uint2*>(p);
+  p += w.items;
+  ws.multi = reinterpret_cast<uint32_t*>(p);
+  p += w.multi;
+  ws.queue = reinterpret_cast<uint32_t*>(p);
   return ws;
 }
 

@@ -136,6 +136,67 @@ __device__ __forceinline__ float wave_sum_range(float v) {
   return v;
 }
 
+// DPP lane permutations within rows of 16 lanes (gfx9 dpp_ctrl encodings).
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+constexpr int kDppQuadXor1 = 0xb1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4e;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+constexpr int kDppRowRor8 = 0x128;     // lane i <- lane (i + 8) % 16 = i ^ 8 within a row
+
+// v + (v of lane ^ 16) and v + (v of lane ^ 32) with the gfx950 permlane
+// swaps (VALU only): swapping a value with itself exchanges rows 0<->1 and
+// 2<->3 (16) or the two 32-lane halves (32), and the two results summed
+// give the pairwise sum in every lane.
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over the 64 / BS lanes {l, l ^ BS, ...} that share lane % BS.
+template <int BS>
+__device__ __forceinline__ float sum_lanes_mod(float v) {
+  if constexpr (BS <= 8) v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
+                                                            __builtin_bit_cast(int, v), kDppRowRor8,
+                                                            0xf, 0xf, false));
+  if constexpr (BS <= 16) v = sum_xor16(v);
+  if constexpr (BS <= 32) v = sum_xor32(v);
+  return v;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Full-wave max / sum with DPP inside each 16-lane row and readlane across
+// the four rows: no LDS round trips. The result is wave-uniform.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppRowMirror>(v));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)),
+               fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp<kDppQuadXor1>(v);
+  v += dpp<kDppQuadXor2>(v);
+  v += dpp<kDppRowHalfMirror>(v);
+  v += dpp<kDppRowMirror>(v);
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
 // Wait until this wave's LDS operations have completed (lgkmcnt(0) only, so
 // outstanding global loads stay in flight), and keep the compiler from
 // moving LDS accesses across the wait.

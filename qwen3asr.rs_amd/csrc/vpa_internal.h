@@ -24,18 +24,28 @@ struct CacheGeom {
   int64_t head_stride;   // elements
 };
 
-// Decode split-K partition length in tokens (a multiple of every supported
-// block size).
+// Decode split-K partition length in tokens of the generic decode kernel (a
+// multiple of every supported block size).
 constexpr int kDecodePartitionTokens = 256;
+// Smallest partition length any decode kernel uses; sizes the workspace.
+constexpr int kDecodeMinPartitionTokens = 128;
 // Upper bound on split-K partitions per sequence handled by the reduce kernel.
 constexpr int kDecodeMaxPartitions = 2048;
 
+// Caller workspace of paged_attention, carved in this order (each piece
+// 256-byte aligned):
 struct DecodeWorkspace {
-  float* part_out;  // [num_seqs, num_heads, max_parts, head_dim]
-  float* part_max;  // [num_seqs, num_heads, max_parts]
-  float* part_sum;  // [num_seqs, num_heads, max_parts]
-  int max_parts;
+  float* part_out;   // [num_seqs, num_heads, max_parts, head_dim] split-K partials
+  float* part_max;   // [num_seqs, num_heads, max_parts]
+  float* part_sum;   // [num_seqs, num_heads, max_parts]
+  uint2* items;      // [num_seqs * max(1, max_parts)] work list {seq << 16 | partition, length}
+  uint32_t* multi;   // [num_seqs] sequences with more than one partition
+  uint32_t* queue;   // [3]: next work unit, number of items, number of multi entries
+  int max_parts;     // ceil(max_context_len / kDecodeMinPartitionTokens)
 };
+
+// Compute units of the current device (cached per device).
+int device_cu_count();
 
 size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len);
 DecodeWorkspace carve_decode_workspace(void* base, int num_seqs, int num_heads, int head_dim,

@@ -10,7 +10,9 @@ from __future__ import annotations
 import ctypes
 import os
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvpa.so")
+# VPA_LIBRARY may point at another build of the same library.
+LIB_PATH = os.environ.get("VPA_LIBRARY") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libvpa.so")
 
 VPA_OK = 0
 VPA_ERR_INVALID_ARGUMENT = 1
