@@ -396,8 +396,12 @@ void paged_decode_rows_kernel(
   }
   const int nblk = (L + BS - 1) / BS;
   const int nchunks = (nblk + PB * NW - 1) / (PB * NW);
-  const int b_begin = (chunk * NW + wave) * PB;
-  const int nb = min(PB, nblk - b_begin);  // <= 0: this wave's partition is past the end
+  // the chunk's blocks are split evenly over the NW waves (at most PB each),
+  // so short sequences keep every wave busy
+  const int c_begin = chunk * PB * NW;
+  const int c_nb = min(PB * NW, nblk - c_begin);
+  const int b_begin = c_begin + (c_nb * wave) / NW;
+  const int nb = c_begin + (c_nb * (wave + 1)) / NW - b_begin;  // 0: idle wave
 
   float acc[G][NVV];
   float m[G], lsum[G];
