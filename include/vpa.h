@@ -128,8 +128,9 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * at graph capture is fine as long as it is >= every context_len).
  * alibi_slopes and sinks must be NULL and softcapping must be 1.0 (the only
  * values vASR passes); anything else returns VPA_ERR_UNSUPPORTED.
- * workspace must hold vpa_paged_attention_workspace_size(...) bytes and be
- * 256-byte aligned; it may be NULL when that size is 0.
+ * workspace must hold vpa_paged_attention_workspace_size(...) bytes (always
+ * non-zero for num_seqs > 0: it carries the per-call work list) and be
+ * 256-byte aligned. Two calls that run concurrently need two workspaces.
  */
 int vpa_paged_attention(void* out, const void* query, const float* k_scale,
                         const float* v_scale, const void* key_cache, const void* value_cache,
@@ -162,6 +163,41 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
                         int64_t num_blocks, int64_t cache_block_stride,
                         int64_t cache_head_stride, int32_t cache_dtype, int32_t out_dtype,
                         void* stream);
+
+/*
+ * chunked_prefill_paged_attention — causal (or full) varlen attention of the
+ * packed prefill queries over the paged cache, without a gathered copy.
+ * Replaces the pair gather_kv_cache + attention::run_attention(q, k, v,
+ * AttentionMask::None, prefill_flash_params(), scaling, true, groups) of
+ * vasr-models/src/model/thinker_text.rs:1344-1365, which runs
+ * flash_attn_varlen over the gathered K/V (attention.rs:554-664); with
+ * causal = 0 it is also the Metal paged_attention_varlen_prefill(q,
+ * key_cache, value_cache, block_tables, context_lens, cu_seqlens_q, k_scale,
+ * v_scale, scale, softcapping = 1) of vasr-paged-attn/src/metal/
+ * varlen_prefill.rs:284-420.
+ *
+ * query/out: [total_query_rows, num_heads, head_dim] packed, bf16 or f16 (the
+ * reference's flash path takes no f32, attention.rs:562). Sequence s owns
+ * query rows cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1 (n_s rows) and its first
+ * L_s = context_lens[s] cached tokens (PagedInputMetadata::context_lens of a
+ * prefill, paged_kv_cache.rs:525-532), the new rows' K/V included (append
+ * them with vpa_reshape_and_cache first). With causal
+ * != 0, query row i sees keys t <= i + L_s - n_s (bottom-right alignment,
+ * attention.rs:78-149); otherwise every t < L_s. A row that sees no key is
+ * written as zeros. n_s and L_s are clamped to max_query_len and
+ * max_kv_len, which size the grid only; rows at or past total_query_rows are
+ * neither read nor written. Block ids >= num_blocks are treated as absent.
+ * out[row, h] = sum_t p_t V[t] / sum_t p_t (no epsilon, as flash attention).
+ * Needs no workspace; safe under stream capture.
+ */
+int vpa_chunked_prefill_paged_attention(
+    void* out, const void* query, const float* k_scale, const float* v_scale,
+    const void* key_cache, const void* value_cache, const uint32_t* block_tables,
+    int32_t block_table_stride, const uint32_t* cu_seqlens_q, const uint32_t* context_lens,
+    int32_t num_seqs, int32_t max_query_len, int32_t max_kv_len, int64_t total_query_rows,
+    float softmax_scale, int32_t causal, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int64_t num_blocks, int64_t cache_block_stride,
+    int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -57,7 +57,7 @@ def lib():
         L.oracle_paged_attention_f64.restype = None
         L.oracle_prefill_attention_f64.argtypes = [_i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i32,
                                                    _i32, _dbl, _i32, _i32, _i32, _i32, _i64,
-                                                   _i64, _i64]
+                                                   _i64, _i64, _dbl]
         L.oracle_prefill_attention_f64.restype = None
         L.cpu_baseline_decode_step.argtypes = [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _p,
                                                _flt, _i32, _i32, _i32, _i32, _i32, _i64, _i64,
@@ -128,8 +128,12 @@ def paged_attention(q, key_cache, value_cache, block_tables, context_lens, max_c
 
 
 def prefill_attention(q, key_cache, value_cache, block_tables, context_lens, cu_seqlens_q, scale,
-                      causal=True, dtype=None) -> np.ndarray:
-    """Chunked prefill attention over the paged cache, float64 [total_q, H, D]."""
+                      causal=True, dtype=None, eps=0.0) -> np.ndarray:
+    """Chunked prefill attention over the paged cache, float64 [total_q, H, D].
+
+    ``eps`` is added to the softmax denominator: 0.0 is the flash varlen path
+    (attention.rs:554-664), 1e-6 the Metal prefill kernel
+    (prefill_paged_attn.metal:1300)."""
     code = dtype_code(q, dtype)
     nb, kvh, d, bs, bstride, hstride = _cache_geom(key_cache)
     tq, h, _ = q.shape
@@ -141,7 +145,7 @@ def prefill_attention(q, key_cache, value_cache, block_tables, context_lens, cu_
                                        _ptr(value_cache), _ptr(block_tables), block_tables.shape[1],
                                        _ptr(context_lens), _ptr(cu_seqlens_q),
                                        block_tables.shape[0], int(bool(causal)), float(scale), h,
-                                       kvh, d, bs, nb, bstride, hstride)
+                                       kvh, d, bs, nb, bstride, hstride, float(eps))
     return out
 
 

@@ -178,7 +178,7 @@ void oracle_gather_kv_cache(int dtype, void* out_key, void* out_value, const voi
  * Attention of one query row against tokens [0, n_keys) of one sequence's
  * kv head, keys/values read through the paged layout, in double:
  *   s_t = scale * q . K_t   (t < n_keys and block valid)
- *   out = sum_t exp(s_t - m) V_t / (sum_t exp(s_t - m) + 1e-6)
+ *   out = sum_t exp(s_t - m) V_t / (sum_t exp(s_t - m) + eps)
  * `logits` is caller scratch of n_keys doubles. Returns 0 if no token is
  * valid (out = 0).
  */
@@ -186,7 +186,7 @@ static void attend_row_f64(int dtype, double* out, const void* q, int64_t q_off,
                            const void* key_cache, const void* value_cache,
                            const uint32_t* bt_row, int64_t n_keys, int head, int head_dim,
                            int block_size, int64_t num_blocks, int64_t block_stride,
-                           int64_t head_stride, double scale, double* logits) {
+                           int64_t head_stride, double scale, double eps, double* logits) {
   const int x = 16 / elem_bytes(dtype);
   double m = -INFINITY;
   for (int64_t t = 0; t < n_keys; ++t) {
@@ -218,7 +218,7 @@ static void attend_row_f64(int dtype, double* out, const void* q, int64_t q_off,
                               value_index(blk, head, d, off, block_size, block_stride,
                                           head_stride));
   }
-  const double inv = 1.0 / (sum + 1e-6);
+  const double inv = 1.0 / (sum + eps);
   for (int d = 0; d < head_dim; ++d) out[d] *= inv;
 }
 
@@ -254,7 +254,7 @@ void oracle_paged_attention_f64(int dtype, double* out, const void* query,
         attend_row_f64(dtype, out + ((int64_t)s * num_heads + h) * head_dim, query,
                        ((int64_t)s * num_heads + h) * head_dim, key_cache, value_cache,
                        block_tables + (int64_t)s * block_table_stride, L, h / group, head_dim,
-                       block_size, num_blocks, block_stride, head_stride, scale, logits);
+                       block_size, num_blocks, block_stride, head_stride, scale, 1e-6, logits);
       }
     }
     free(logits);
@@ -268,6 +268,8 @@ void oracle_paged_attention_f64(int dtype, double* out, const void* query,
  * rows. Query row i sits at absolute position P_s + i with P_s = L_s - n_s;
  * causal: it sees keys t <= P_s + i (attention.rs:78-149); non-causal: every
  * t < L_s (the Metal sibling kernel, prefill_paged_attn.metal:1192-1199).
+ * The softmax denominator is sum + eps: 0 for the flash varlen path the CUDA
+ * build takes (attention.rs:554-664), 1e-6 for the Metal kernel (:1300).
  */
 void oracle_prefill_attention_f64(int dtype, double* out, const void* query,
                                   const void* key_cache, const void* value_cache,
@@ -276,7 +278,7 @@ void oracle_prefill_attention_f64(int dtype, double* out, const void* query,
                                   int num_seqs, int causal, double scale, int num_heads,
                                   int num_kv_heads, int head_dim, int block_size,
                                   int64_t num_blocks, int64_t block_stride,
-                                  int64_t head_stride) {
+                                  int64_t head_stride, double eps) {
   const int group = num_heads / num_kv_heads;
   for (int s = 0; s < num_seqs; ++s) {
     const int64_t n = (int64_t)cu_seqlens_q[s + 1] - cu_seqlens_q[s];
@@ -295,7 +297,7 @@ void oracle_prefill_attention_f64(int dtype, double* out, const void* query,
           attend_row_f64(dtype, out + (row * num_heads + h) * head_dim, query,
                          (row * num_heads + h) * head_dim, key_cache, value_cache,
                          block_tables + (int64_t)s * block_table_stride, nk, h / group,
-                         head_dim, block_size, num_blocks, block_stride, head_stride, scale,
+                         head_dim, block_size, num_blocks, block_stride, head_stride, scale, eps,
                          logits);
         }
       }

@@ -334,4 +334,67 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
                                                static_cast<hipStream_t>(stream)));
 }
 
+int vpa_chunked_prefill_paged_attention(
+    void* out, const void* query, const float* k_scale, const float* v_scale,
+    const void* key_cache, const void* value_cache, const uint32_t* block_tables,
+    int32_t block_table_stride, const uint32_t* cu_seqlens_q, const uint32_t* context_lens,
+    int32_t num_seqs, int32_t max_query_len, int32_t max_kv_len, int64_t total_query_rows,
+    float softmax_scale, int32_t causal, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int64_t num_blocks, int64_t cache_block_stride,
+    int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype, void* stream) {
+  (void)k_scale;
+  (void)v_scale;
+  clear_error();
+  const char* op = "chunked_prefill_paged_attention";
+  if (dtype != cache_dtype)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from query dtype %s", op,
+                dtype_name(cache_dtype), dtype_name(dtype));
+  int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
+                       cache_block_stride, cache_head_stride, key_cache, value_cache);
+  if (rc != VPA_OK) return rc;
+  if (num_seqs < 0 || num_heads <= 0 || max_query_len < 0 || max_kv_len < 0 ||
+      total_query_rows < 0 || block_table_stride < 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: bad sizes num_seqs=%d num_heads=%d max_query_len=%d max_kv_len=%d "
+                "total_query_rows=%lld block_table_stride=%d",
+                op, num_seqs, num_heads, max_query_len, max_kv_len,
+                (long long)total_query_rows, block_table_stride);
+  if (num_heads % num_kv_heads != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: num_heads=%d not a multiple of num_kv_heads=%d",
+                op, num_heads, num_kv_heads);
+  const int group = num_heads / num_kv_heads;
+  if (!prefill_supported(dtype, head_dim, block_size, group))
+    return fail(VPA_ERR_UNSUPPORTED,
+                "%s: no MFMA kernel for dtype=%s head_dim=%d block_size=%d group=%d (bf16/f16, "
+                "head_dim 64/128, block_size 8/16/32, 1/2/4 query heads per kv head)",
+                op, dtype_name(dtype), head_dim, block_size, group);
+  if (num_seqs == 0 || max_query_len == 0 || total_query_rows == 0) return VPA_OK;
+  {
+    const int ppb = prefill_positions_per_workgroup(group);
+    const int64_t grid =
+        (int64_t)num_seqs * ((max_query_len + ppb - 1) / ppb) * (int64_t)num_kv_heads;
+    if (grid > ((int64_t)1 << 31) - 1)
+      return fail(VPA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups exceeds 2^31-1", op,
+                  (long long)grid);
+  }
+  if (out == nullptr || query == nullptr || block_tables == nullptr ||
+      cu_seqlens_q == nullptr || context_lens == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: out, query, block_tables, cu_seqlens_q and context_lens must be non-null",
+                op);
+  if (!aligned16(out) || !aligned16(query))
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: out and query must be 16-byte aligned", op);
+  if (max_kv_len > 0 && (int64_t)block_table_stride * block_size < max_kv_len)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: block_table_stride=%d too small for max_kv_len=%d (block_size=%d)", op,
+                block_table_stride, max_kv_len, block_size);
+  CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
+              cache_head_stride};
+  return hip_status(op, launch_prefill_paged(dtype, out, query, key_cache, value_cache,
+                                             block_tables, block_table_stride, cu_seqlens_q,
+                                             context_lens, num_seqs, max_query_len, max_kv_len,
+                                             total_query_rows, softmax_scale, causal, num_heads,
+                                             g, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

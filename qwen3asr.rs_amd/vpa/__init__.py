@@ -10,6 +10,7 @@ from .ops import (  # noqa: F401
     cache_geometry,
     gather_kv_cache,
     paged_attention,
+    paged_attention_varlen_prefill,
     paged_attention_workspace,
     reshape_and_cache,
 )
@@ -19,6 +20,7 @@ __all__ = [
     "cache_geometry",
     "gather_kv_cache",
     "paged_attention",
+    "paged_attention_varlen_prefill",
     "paged_attention_workspace",
     "reshape_and_cache",
 ]

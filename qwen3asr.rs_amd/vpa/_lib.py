@@ -47,6 +47,9 @@ SIGNATURES = {
                                            _i64, _i32, _i32, _p, _sz, _p]),
     "vpa_gather_kv_cache": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _i32, _i64, _i32,
                                            _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
+    "vpa_chunked_prefill_paged_attention": (ctypes.c_int, [
+        _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i64, _f32, _i32, _i32,
+        _i32, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
 }
 
 

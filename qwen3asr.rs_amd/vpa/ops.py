@@ -216,3 +216,61 @@ def gather_kv_cache(key_cache: torch.Tensor, value_cache: torch.Tensor,
         cu_seqlens_kv.data_ptr(), num_seqs, total_tokens, kvh, d, bs, nb, bstride, hstride,
         dtype_code(key_cache.dtype), dtype_code(out_dtype), _stream(key_cache)))
     return out_k, out_v
+
+
+def paged_attention_varlen_prefill(q: torch.Tensor, key_cache: torch.Tensor,
+                                   value_cache: torch.Tensor, block_tables: torch.Tensor,
+                                   context_lens: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                                   k_scale: Optional[torch.Tensor], v_scale: Optional[torch.Tensor],
+                                   scale: float, softcapping: float, *, causal: bool = False,
+                                   max_query_len: Optional[int] = None,
+                                   max_context_len: Optional[int] = None,
+                                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Varlen prefill attention of packed queries over the paged cache.
+
+    Argument order and meaning follow the reference's Metal op
+    (``vasr-paged-attn/src/metal/varlen_prefill.rs:284-295``), which is
+    non-causal; ``causal=True`` gives the bottom-right causal attention that
+    the CUDA build computes with gather_kv_cache + flash varlen
+    (``thinker_text.rs:1344-1365``). ``q`` is [total_q, H, D] bf16/f16;
+    sequence s owns rows cu_seqlens_q[s]..cu_seqlens_q[s+1]-1 and the first
+    context_lens[s] cached tokens (its own new tokens included). The maxima
+    size the grid; a caller that knows them on the host passes them to skip
+    a device read. Returns [total_q, H, D]."""
+    _require_device(q, key_cache, value_cache, block_tables, context_lens, cu_seqlens_q)
+    nb, kvh, d, bs, bstride, hstride = cache_geometry(key_cache, value_cache)
+    if softcapping != 1.0:
+        raise VpaError(_lib.VPA_ERR_UNSUPPORTED, f"softcapping must be 1.0, got {softcapping}")
+    if q.dim() != 3 or q.shape[2] != d:
+        raise _err(f"q must be [total_q, H, {d}], got {tuple(q.shape)}")
+    tq, h, _ = q.shape
+    if block_tables.dtype != torch.uint32 or block_tables.dim() != 2:
+        raise _err(f"block_tables must be u32 2-d, got {block_tables.dtype} "
+                   f"{tuple(block_tables.shape)}")
+    num_seqs = block_tables.shape[0]
+    if cu_seqlens_q.dtype != torch.uint32 or cu_seqlens_q.shape != (num_seqs + 1,):
+        raise _err(f"cu_seqlens_q must be u32 [{num_seqs + 1}], got {cu_seqlens_q.dtype} "
+                   f"{tuple(cu_seqlens_q.shape)}")
+    if context_lens.dtype != torch.uint32 or context_lens.shape != (num_seqs,):
+        raise _err(f"context_lens must be u32 [{num_seqs}], got {context_lens.dtype} "
+                   f"{tuple(context_lens.shape)}")
+    if max_query_len is None:
+        max_query_len = int((cu_seqlens_q[1:].long() - cu_seqlens_q[:-1].long()).max().item()) \
+            if num_seqs else 0
+    if max_context_len is None:
+        max_context_len = int(context_lens.long().max().item()) if num_seqs else 0
+    q = q.contiguous()
+    block_tables = block_tables.contiguous()
+    context_lens = context_lens.contiguous()
+    cu_seqlens_q = cu_seqlens_q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise _err("out must be a contiguous tensor shaped and typed like q")
+    check(_lib.load().vpa_chunked_prefill_paged_attention(
+        out.data_ptr(), q.data_ptr(), _ptr(k_scale), _ptr(v_scale), key_cache.data_ptr(),
+        value_cache.data_ptr(), block_tables.data_ptr(), block_tables.shape[1],
+        cu_seqlens_q.data_ptr(), context_lens.data_ptr(), num_seqs, int(max_query_len),
+        int(max_context_len), tq, float(scale), int(bool(causal)), h, kvh, d, bs, nb, bstride,
+        hstride, dtype_code(q.dtype), dtype_code(key_cache.dtype), _stream(q)))
+    return out

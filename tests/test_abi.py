@@ -162,3 +162,42 @@ def test_gather_host_validation():
                                  16, 100, 8 * 128 * 16, 128 * 16, _lib.DTYPE_BF16,
                                  _lib.DTYPE_BF16, None)
     assert rc == 0
+
+
+def pf_call(**over):
+    args = dict(out=FAKE, q=FAKE, ks=None, vs=None, kc=FAKE, vc=FAKE, bt=FAKE, bts=64,
+                cuq=FAKE, cl=FAKE, b=4, maxq=512, maxkv=1024, tq=2048, scale=0.088, causal=1,
+                h=16, kvh=8, d=128, bs=16, nb=100, bstride=8 * 128 * 16, hstride=128 * 16,
+                dtype=_lib.DTYPE_BF16, cdtype=_lib.DTYPE_BF16, stream=None)
+    args.update(over)
+    lib = _lib.load()
+    rc = lib.vpa_chunked_prefill_paged_attention(*args.values())
+    return rc, lib.vpa_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,needle", [
+    (dict(dtype=_lib.DTYPE_F32, cdtype=_lib.DTYPE_F32, bstride=8 * 128 * 16 * 2,
+          hstride=128 * 16 * 2), _lib.VPA_ERR_UNSUPPORTED, "no MFMA kernel"),
+    (dict(d=256, bstride=8 * 256 * 16, hstride=256 * 16), _lib.VPA_ERR_UNSUPPORTED,
+     "no MFMA kernel"),
+    (dict(h=64), _lib.VPA_ERR_UNSUPPORTED, "no MFMA kernel"),
+    (dict(h=12), _lib.VPA_ERR_INVALID_ARGUMENT, "multiple"),
+    (dict(cdtype=_lib.DTYPE_F16), _lib.VPA_ERR_UNSUPPORTED, "differs"),
+    (dict(bts=10), _lib.VPA_ERR_INVALID_ARGUMENT, "block_table_stride"),
+    (dict(cuq=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
+    (dict(cl=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
+    (dict(out=FAKE + 8), _lib.VPA_ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(maxq=-1), _lib.VPA_ERR_INVALID_ARGUMENT, "bad sizes"),
+    (dict(tq=-5), _lib.VPA_ERR_INVALID_ARGUMENT, "bad sizes"),
+    (dict(hstride=100), _lib.VPA_ERR_INVALID_ARGUMENT, "strides"),
+])
+def test_prefill_host_validation(over, code, needle):
+    rc, msg = pf_call(**over)
+    assert rc == code, msg
+    assert needle in msg
+
+
+def test_prefill_empty_is_noop():
+    assert pf_call(b=0, out=None, q=None)[0] == 0
+    assert pf_call(maxq=0)[0] == 0
+    assert pf_call(tq=0)[0] == 0

@@ -251,6 +251,9 @@ def test_prefill_oracle_matches_torch_sdpa_with_cached_mask(causal):
     q, kc, vc, bt, lens, cu = _prefill_case(rng, code, h, kvh, d, bs, prior, qlens, nb)
     scale = d ** -0.5
     got = orc.prefill_attention(q, kc, vc, bt, lens, cu, scale, causal=causal, dtype=code)
+    got_eps = orc.prefill_attention(q, kc, vc, bt, lens, cu, scale, causal=causal, dtype=code,
+                                    eps=1e-6)
+    assert not np.array_equal(got, got_eps)
     for s in range(len(lens)):
         L, n, P = int(lens[s]), qlens[s], prior[s]
         ki, vi = inverse_layout(kc, vc, bt[s, :(L + bs - 1) // bs], L)
@@ -268,7 +271,10 @@ def test_prefill_oracle_matches_torch_sdpa_with_cached_mask(causal):
         m = logits.max(dim=-1, keepdim=True).values
         S = torch.exp(torch.logsumexp(logits, dim=-1, keepdim=True) - m)
         g = torch.from_numpy(got[cu[s]:cu[s + 1]]).transpose(0, 1)
-        torch.testing.assert_close(g * (S + 1e-6) / S, want, rtol=1e-10, atol=1e-12)
+        torch.testing.assert_close(g, want, rtol=1e-10, atol=1e-12)
+        # the Metal kernel's epsilon variant divides by S + 1e-6
+        ge = torch.from_numpy(got_eps[cu[s]:cu[s + 1]]).transpose(0, 1)
+        torch.testing.assert_close(ge * (S + 1e-6) / S, want, rtol=1e-10, atol=1e-12)
     if prior[0] == 0 and causal:
         # P = 0 reduces to plain causal attention
         L = qlens[0]
@@ -295,8 +301,8 @@ def test_prefill_cached_causal_mask_kat():
     q = np.ones((2, h, d), dtype=np.float32)
     out = orc.prefill_attention(q, kc, vc, bt, np.array([5], dtype=np.uint32),
                                 np.array([0, 2], dtype=np.uint32), 1.0, causal=True, dtype=code)
-    np.testing.assert_allclose(out[0, 0, :5], np.array([1, 1, 1, 1, 0]) / (4 + 1e-6), rtol=1e-12)
-    np.testing.assert_allclose(out[1, 0, :5], np.ones(5) / (5 + 1e-6), rtol=1e-12)
+    np.testing.assert_allclose(out[0, 0, :5], np.array([1, 1, 1, 1, 0]) / 4, rtol=1e-12)
+    np.testing.assert_allclose(out[1, 0, :5], np.ones(5) / 5, rtol=1e-12)
 
 
 def test_prefill_matches_reference_packed_vs_unpacked_kat():
