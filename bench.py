@@ -31,6 +31,7 @@ for _p in (ROOT, os.path.join(ROOT, "qwen3asr.rs_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 METRIC = "paged-attn decode HBM GB/s (% of peak) + KV-append GB/s at Qwen3-ASR shapes"
 
 
@@ -44,6 +45,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU baseline budget (0 disables it)")
     ap.add_argument("--seed", type=int, default=None)
+    ap.add_argument("--no-prefill", dest="prefill", action="store_false",
+                    help="skip the c4 chunked-prefill measurement")
     return ap.parse_args()
 
 
@@ -152,6 +155,73 @@ def cpu_baseline(w, layers, budget_s):
     }
 
 
+def prefill_c4(dev, reps=10):
+    """Row a3 measured alongside the headline: c4 (64 sequences x 512 new
+    tokens over 0..1024 prior tokens, bf16) append with reshape_and_cache,
+    then causal chunked-prefill attention over the paged cache; HIP events
+    around each op on the current stream, after 2 untimed calls."""
+    import numpy as np
+    import torch
+
+    import vpa
+    from vpa import workloads
+
+    w = workloads.c4()
+    h, kvh, d, bs = w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    g = torch.Generator(device=dev)
+    g.manual_seed(w.seed)
+    bf = torch.bfloat16
+    kc = torch.randn((w.num_blocks, kvh, d // 8, bs, 8), generator=g, device=dev, dtype=bf)
+    vc = torch.randn((w.num_blocks, kvh, d, bs), generator=g, device=dev, dtype=bf)
+    tq = int(w.query_lens.sum())
+    q = torch.randn((tq, h, d), generator=g, device=dev, dtype=bf)
+    kn = torch.randn((tq, kvh, d), generator=g, device=dev, dtype=bf)
+    vn = torch.randn((tq, kvh, d), generator=g, device=dev, dtype=bf)
+    slots = torch.from_numpy(w.slot_mapping()).to(dev)
+    bt = torch.from_numpy(w.block_tables.astype(np.uint32)).to(dev)
+    cl = torch.from_numpy(w.context_lens).to(dev)
+    cu = torch.from_numpy(w.cu_seqlens_q).to(dev)
+    out = torch.empty_like(q)
+    mq, mk = int(w.query_lens.max()), int(w.context_lens.max())
+
+    def append():
+        vpa.reshape_and_cache(kn, vn, None, None, kc, vc, slots)
+
+    def prefill():
+        vpa.paged_attention_varlen_prefill(q, kc, vc, bt, cl, cu, None, None, d ** -0.5, 1.0,
+                                           causal=True, max_query_len=mq, max_context_len=mk,
+                                           out=out)
+
+    res = {}
+    for name, fn in (("append", append), ("prefill", prefill)):
+        for _ in range(2):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) * 1e3 / reps  # us per call
+    app_bytes = 2 * tq * 2 * kvh * d * 2 + 8 * tq
+    flops = w.flops()
+    tflops = flops / (res["prefill"] * 1e-6) / 1e12
+    return {
+        "workload": "c4",
+        "append_us": round(res["append"], 2),
+        "append_gbps": round(app_bytes / (res["append"] * 1e-6) / 1e9, 2),
+        "append_frac_of_peak": round(app_bytes / (res["append"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "prefill_us": round(res["prefill"], 2),
+        "prefill_tflops": round(tflops, 2),
+        "roofline": {"kernel": "chunked_prefill_paged_attention", "bound": "mfma",
+                     "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "algorithmic_flops_per_launch": flops},
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -213,6 +283,11 @@ def main():
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(w, layers, args.cpu_seconds)
+    pf = None
+    if args.prefill:
+        del layers, ws
+        torch.cuda.empty_cache()
+        pf = prefill_c4(dev)
 
     line = {
         "metric": METRIC,
@@ -256,6 +331,7 @@ def main():
             "us_per_launch": round(dec_launch_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
+        "prefill_c4": pf,
     }
     print(json.dumps(line), flush=True)
 

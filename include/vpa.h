@@ -29,7 +29,7 @@
  *     vpa_paged_attention_workspace_size).
  *   - `stream` is a hipStream_t (NULL = the null stream).
  *   - The library is reentrant; its only global state is the thread-local
- *     error message.
+ *     error message and a per-device cache of the compute-unit count.
  */
 #ifndef VPA_H_
 #define VPA_H_

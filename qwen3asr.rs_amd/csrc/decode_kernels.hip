@@ -265,29 +265,35 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
 // chunks per key row).
 //
 // Work list: decode_plan_kernel (one workgroup) turns context_lens into the
-// list of (sequence, partition) items of PT tokens, resets the work queue and
-// the per-(sequence, kv head) completion counters. All of it lives in the
-// caller's workspace and is rebuilt by every call, so the pair of launches
-// can be captured in a graph and replayed with new lengths.
+// sequence-ordered list of (sequence, chunk) items, a chunk being NW * PT
+// tokens, plus the list of sequences that span several chunks and a small
+// header {0, item count, multi count}. All of it lives in the caller's
+// workspace and is rebuilt by every call, so the launches can be captured
+// in a graph and replayed with new lengths; max_context_len only sizes the
+// grid, surplus workgroups exit at once.
 //
-// paged_decode_rows_kernel: persistent wavefronts take (item, kv head) work
-// units from the queue with one atomic per unit, so no workgroup is spent on
-// partitions past a sequence's end and short and long sequences balance
-// automatically. Per unit, with no cross-lane reduction in the loops:
-//   K pass: 64 / BS blocks per iteration, lane l owns token l % BS of block
-//     l / BS and loads its whole key row (the D/8 chunks at stride BS*16 B;
-//     16 lanes x 16 B = 256 B contiguous per chunk and block). q of the G
-//     heads is staged in LDS and read as broadcasts. Logits go to LDS.
-//   softmax: DPP max / sum over the partition; probabilities are stored in
-//     LDS rounded to the cache type.
-//   V pass: each load instruction reads 1 KiB contiguous of a value tile;
-//     lane l owns rows l / (BS/8) + k * 64 / (BS/8) over 8 tokens, and the
-//     BS/8 lanes of a row are summed with DPP once at the end.
-// A sequence with several partitions writes f32 partials, merged by
-// decode_merge_kernel over the plan's list of multi-partition sequences.
-// (Merging in the last wave to finish would need an agent-scope release per
-// partition, which on gfx950 writes back the whole L2: far more expensive
-// than one extra launch.)
+// paged_decode_rows_kernel: one workgroup of NW waves per (item, kv head);
+// the chunk's blocks are split evenly over the waves (up to PT tokens each).
+// Per wave, with no cross-lane reduction inside the loops:
+//   K pass: stages of 8 16-byte loads per lane, double-buffered; load k of a
+//     key tile gives lane l vector l + 64 k, i.e. token l % BS and chunk
+//     l / BS + k * (64 / BS), so every instruction reads 1 KiB contiguous and
+//     the lane needs only those chunks of q (held in registers). The partial
+//     dot products of a token are summed over its 64 / BS lanes with DPP and
+//     permlane swaps; logits go to LDS. The first two V stages are issued
+//     during the last K stages.
+//   softmax: DPP max / sum over the wave's tokens; probabilities are stored
+//     in LDS rounded to the cache type.
+//   V pass: same 1 KiB-per-instruction loads of the value tiles; lane l owns
+//     rows l / (BS/8) + k * 64 / (BS/8) over 8 tokens, and the BS/8 lanes of
+//     a row are summed with DPP once at the end.
+// The NW partial results are merged in LDS. A sequence of a single chunk
+// writes its output directly; a longer one writes one f32 partial row per
+// chunk (D values + a 32-float line holding {max, sum}, whole 128-byte
+// lines), merged by decode_merge_kernel over the plan's list of multi-chunk
+// sequences. (Merging in the last workgroup to finish would need an
+// agent-scope release per chunk, which on gfx950 writes back the whole L2:
+// far more expensive than one extra launch.)
 // ---------------------------------------------------------------------------
 // Floats per split-K partial row of the rows path: D outputs + a 32-float
 // line holding {max, sum}.

@@ -61,11 +61,22 @@ __device__ __forceinline__ float max_xor32(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-constexpr int kPrefillKeys = 32;    // keys per LDS tile
+#ifndef VPA_PREFILL_KEYS
+#define VPA_PREFILL_KEYS 32
+#endif
+#ifndef VPA_PREFILL_COLS
+#define VPA_PREFILL_COLS 1
+#endif
+constexpr int kPrefillKeys = VPA_PREFILL_KEYS;       // keys per LDS tile (32 or 64)
+constexpr int kPrefillColGroups = VPA_PREFILL_COLS;  // 32-row query groups per wave (1 or 2)
+#ifndef VPA_PREFILL_WAVES_PER_EU
+#define VPA_PREFILL_WAVES_PER_EU 2
+#endif
 constexpr int kPrefillThreads = 256;
 
 template <typename T, int D, int BS, int G>
-__global__ __launch_bounds__(kPrefillThreads) void prefill_paged_kernel(
+__global__ __launch_bounds__(kPrefillThreads)
+__attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_paged_kernel(
     T* __restrict__ out, const T* __restrict__ query, const T* __restrict__ key_cache,
     const T* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
     int32_t block_table_stride, const uint32_t* __restrict__ cu_seqlens_q,
@@ -74,27 +85,37 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_paged_kernel(
     int32_t num_heads, int32_t num_kv_heads, int64_t num_blocks, int64_t block_stride,
     int64_t head_stride, int32_t q_tiles) {
   constexpr int KT = kPrefillKeys;
+  constexpr int CG = kPrefillColGroups;
   constexpr int X = 8;          // 16-bit elements per 16-byte key vector
-  constexpr int PPW = 32 / G;   // query positions per wave
+  constexpr int ROWS = 32 * CG; // query rows per wave
+  constexpr int PPW = ROWS / G; // query positions per wave
   constexpr int PPB = 4 * PPW;  // query positions per workgroup
+  constexpr int KG = KT / 32;   // 32-key groups of a tile
   constexpr int KS = D / 16;    // k-steps of Q.K^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
-  constexpr int VROW = KT + 4;  // LDS value row: 72 bytes keeps the b64 reads conflict-light
-  constexpr int UPT = D / 64;   // 16-byte units per thread per K (and per V) tile
+  constexpr int VROW = KT + 4;  // LDS value row (elements): +8 bytes keeps b64 reads conflict-light
+  constexpr int UPT = KT * D / 8 / kPrefillThreads;  // 16-byte units per thread per K / V tile
+  constexpr int KSTEP = kPrefillThreads / KT;        // chunk stride of a thread's K units
+  constexpr int OCT = KT / 8;                        // 8-key octets per value row
+  constexpr int VSTEP = kPrefillThreads / OCT;       // dim stride of a thread's V units
   static_assert(BS >= 8 && (KT % BS == 0 || BS % KT == 0), "block size");
-  static_assert(kPrefillThreads % KT == 0 && D % 64 == 0, "tile shape");
+  static_assert((KT == 32 || KT == 64) && (CG == 1 || CG == 2) && UPT >= 1, "tile shape");
+  static_assert(ROWS % G == 0 && D % 32 == 0, "rows");
 
   __shared__ __align__(16) uint4 s_k[2][D / X][KT];  // [chunk of 8 dims][key]
   __shared__ __align__(16) uint16_t s_v[2][D][VROW];  // [dim][key]
-  __shared__ uint32_t s_valid[2];                     // keys of the tile that exist
+  __shared__ uint64_t s_valid[2];                     // keys of the tile that exist
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  // consecutive workgroups: kv heads, then the query tiles of one sequence
+  // (heaviest first), so the tiles of a (sequence, kv head) run together on
+  // one XCD and share its K/V through L2
   const int j = (int)(blockIdx.x % (uint32_t)num_kv_heads);
   const int rest = (int)(blockIdx.x / (uint32_t)num_kv_heads);
-  const int s = rest % num_seqs;
-  const int qt = q_tiles - 1 - rest / num_seqs;  // last (longest) query tiles first
+  const int s = rest / q_tiles;
+  const int qt = q_tiles - 1 - rest % q_tiles;
 
   const uint32_t qa = cu_seqlens_q[s], qb = cu_seqlens_q[s + 1];
   int q_len = qb > qa ? (int)min(qb - qa, (uint32_t)max_query_len) : 0;
@@ -109,45 +130,58 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_paged_kernel(
   const int n_keys = max(0, causal ? min(k_len, wg_end + shift) : k_len);
   const int n_tiles = (n_keys + KT - 1) / KT;
 
-  // this lane's query row (column of S^T and O^T)
+  // this lane's query rows (one per column group; column of S^T and O^T)
   const int col = lane & 31;
   const int half = lane >> 5;
   const int wpos0 = p0 + wave * PPW;
-  const int pos = wpos0 + col % PPW;
-  const int head = j * G + col / PPW;
-  const bool row_ok = pos < q_len;
-  const int64_t row = (int64_t)qa + pos;
-  const int limit = causal ? pos + shift : k_len - 1;  // last key the row sees
+  bool row_ok[CG];
+  int64_t row[CG];
+  int head[CG], limit[CG];
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) {
+    const int ri = cg * 32 + col;
+    const int pos = wpos0 + ri % PPW;
+    head[cg] = j * G + ri / PPW;
+    row_ok[cg] = pos < q_len;
+    row[cg] = (int64_t)qa + pos;
+    limit[cg] = causal ? pos + shift : k_len - 1;  // last key the row sees
+  }
   const int wave_end = min(wpos0 + PPW, q_len);
   const int wave_keys =
       wave_end <= wpos0 ? 0 : max(0, causal ? min(k_len, wave_end + shift) : k_len);
   const int wave_min_limit = causal ? wpos0 + shift : k_len - 1;
 
-  uint4 qop[KS];
-  {
-    const T* qrow = query + (row * num_heads + head) * D + 8 * half;
+  uint4 qop[CG][KS];
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) {
+    const T* qrow = query + (row[cg] * num_heads + head[cg]) * D + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      qop[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks) : make_uint4(0, 0, 0, 0);
+      qop[cg][ks] =
+          row_ok[cg] ? *reinterpret_cast<const uint4*>(qrow + 16 * ks) : make_uint4(0, 0, 0, 0);
   }
 
-  f32x16_t o[DT];
+  f32x16_t o[CG][DT];
+  float m[CG], lsum[CG];  // running max (log2 units) and this lane's share of the sum
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+  for (int cg = 0; cg < CG; ++cg) {
+    m[cg] = -INFINITY;
+    lsum[cg] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
-  float m = -INFINITY;  // running max of the row, log2 units
-  float lsum = 0.f;     // this lane's share of the row's exp sum
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[cg][dt][e] = 0.f;
+  }
 
   const T* kbase = key_cache + (int64_t)j * head_stride;
   const T* vbase = value_cache + (int64_t)j * head_stride;
   const uint32_t* bt = block_tables + (int64_t)s * block_table_stride;
-  // loader roles: K units hold key tid % KT, chunks tid / KT + 8 i; V units
-  // hold keys 8 (tid % 4) .. +7 of dims tid / 4 + 64 i
+  // loader roles: K units hold key tid % KT of chunks tid / KT + KSTEP i;
+  // V units hold keys 8 (tid % OCT) .. +7 of dims tid / OCT + VSTEP i
   const int lk = tid % KT;
   const int lc = tid / KT;
-  const int lo = tid % 4;
-  const int ld = tid / 4;
+  const int lo = tid % OCT;
+  const int ld = tid / OCT;
   uint4 kreg[UPT], vreg[UPT];
   bool kvalid = false;
 
@@ -161,7 +195,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_paged_kernel(
       const T* src = kbase + (int64_t)phys * block_stride + (key % BS) * X;
 #pragma unroll
       for (int i = 0; i < UPT; ++i)
-        kreg[i] = *reinterpret_cast<const uint4*>(src + (int64_t)(lc + 8 * i) * BS * X);
+        kreg[i] = *reinterpret_cast<const uint4*>(src + (int64_t)(lc + KSTEP * i) * BS * X);
     }
     {
       const int key = k0 + 8 * lo;
@@ -171,7 +205,7 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_paged_kernel(
       const T* src = vbase + (int64_t)phys * block_stride + (key % BS);
 #pragma unroll
       for (int i = 0; i < UPT; ++i)
-        vreg[i] = *reinterpret_cast<const uint4*>(src + (int64_t)(ld + 64 * i) * BS);
+        vreg[i] = *reinterpret_cast<const uint4*>(src + (int64_t)(ld + VSTEP * i) * BS);
       // values of keys that do not exist are zeroed (stale cache contents
       // could be NaN, and 0 * NaN would poison the sum)
       const int nvalid = ok ? min(8, k_len - key) : 0;
@@ -189,71 +223,94 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_paged_kernel(
   };
   auto store_tile = [&](int b) {
 #pragma unroll
-    for (int i = 0; i < UPT; ++i) s_k[b][lc + 8 * i][lk] = kreg[i];
+    for (int i = 0; i < UPT; ++i) s_k[b][lc + KSTEP * i][lk] = kreg[i];
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
-      uint2* dst = reinterpret_cast<uint2*>(&s_v[b][ld + 64 * i][8 * lo]);
+      uint2* dst = reinterpret_cast<uint2*>(&s_v[b][ld + VSTEP * i][8 * lo]);
       dst[0] = make_uint2(vreg[i].x, vreg[i].y);
       dst[1] = make_uint2(vreg[i].z, vreg[i].w);
     }
-    // lanes 0..31 of wave 0 hold keys 0..31 of the tile
+    // lanes 0..KT-1 of wave 0 hold keys 0..KT-1 of the tile
     if (wave == 0) {
       const uint64_t bal = __ballot(kvalid);
-      if (lane == 0) s_valid[b] = (uint32_t)bal;
+      if (lane == 0) s_valid[b] = KT == 64 ? bal : (bal & 0xffffffffull);
     }
   };
   auto compute_tile = [&](int tt, int b) {
     const int k0 = tt * KT;
     if (k0 >= wave_keys) return;  // no row of this wave sees these keys
-    const uint32_t vmask = s_valid[b];
-    f32x16_t sacc;
+    const uint64_t vmask = s_valid[b];
+    const bool full =
+        vmask == (KT == 64 ? ~0ull : 0xffffffffull) && k0 + KT - 1 <= wave_min_limit;
+    // S^T = K . Q^T: every K operand read from LDS feeds CG MFMAs
+    f32x16_t sacc[KG][CG];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+    for (int kg = 0; kg < KG; ++kg)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      sacc = mfma32x32x16<T>(s_k[b][2 * ks + half][col], qop[ks], sacc);
-    const bool full = vmask == 0xffffffffu && k0 + KT - 1 <= wave_min_limit;
-    float sv[16];
-    float mx = -INFINITY;
+      for (int cg = 0; cg < CG; ++cg)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = 8 * (r / 4) + 4 * half + (r % 4);  // accumulator row of element r
-      float v = sacc[r] * scale_log2;
-      if (!full) v = (((vmask >> key) & 1u) && k0 + key <= limit) ? v : -INFINITY;
-      sv[r] = v;
-      mx = fmaxf(mx, v);
+        for (int e = 0; e < 16; ++e) sacc[kg][cg][e] = 0.f;
+#pragma unroll
+    for (int kg = 0; kg < KG; ++kg)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint4 a = s_k[b][2 * ks + half][32 * kg + col];
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg)
+          sacc[kg][cg] = mfma32x32x16<T>(a, qop[cg][ks], sacc[kg][cg]);
+      }
+    // online softmax per row; P^T operands straight from the accumulators
+    uint4 pk[CG][2 * KG];
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+      float sv[KG][16];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kg = 0; kg < KG; ++kg)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = 32 * kg + 8 * (r / 4) + 4 * half + (r % 4);  // row of element r
+          float v = sacc[kg][cg][r] * scale_log2;
+          if (!full) v = (((vmask >> key) & 1ull) && k0 + key <= limit[cg]) ? v : -INFINITY;
+          sv[kg][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = max_xor32(mx);
+      const float m_new = fmaxf(m[cg], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m[cg] - m_use);
+      float ps = 0.f;
+#pragma unroll
+      for (int kg = 0; kg < KG; ++kg)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sv[kg][r] = exp2f(sv[kg][r] - m_use);
+          ps += sv[kg][r];
+        }
+      lsum[cg] = lsum[cg] * alpha + ps;
+      m[cg] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[cg][dt][e] *= alpha;
+#pragma unroll
+      for (int k2 = 0; k2 < 2 * KG; ++k2) {
+        const float* p = &sv[k2 / 2][8 * (k2 % 2)];
+        pk[cg][k2] = make_uint4(pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]),
+                                pack2<T>(p[4], p[5]), pack2<T>(p[6], p[7]));
+      }
     }
-    mx = max_xor32(mx);
-    const float m_new = fmaxf(m, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m - m_use);
-    float ps = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      sv[r] = exp2f(sv[r] - m_use);
-      ps += sv[r];
-    }
-    lsum = lsum * alpha + ps;
-    m = m_new;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-    uint4 pk[2];
-#pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2)
-      pk[k2] = make_uint4(pack2<T>(sv[8 * k2 + 0], sv[8 * k2 + 1]),
-                          pack2<T>(sv[8 * k2 + 2], sv[8 * k2 + 3]),
-                          pack2<T>(sv[8 * k2 + 4], sv[8 * k2 + 5]),
-                          pack2<T>(sv[8 * k2 + 6], sv[8 * k2 + 7]));
+    // O^T += V^T . P^T: k-step k2 covers keys 16 k2 + {4h..4h+3, 8+4h..8+4h+3}
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
+      for (int k2 = 0; k2 < 2 * KG; ++k2) {
         const uint16_t* vr = &s_v[b][32 * dt + col][16 * k2 + 4 * half];
         const uint2 lo4 = *reinterpret_cast<const uint2*>(vr);
         const uint2 hi4 = *reinterpret_cast<const uint2*>(vr + 8);
-        o[dt] = mfma32x32x16<T>(make_uint4(lo4.x, lo4.y, hi4.x, hi4.y), pk[k2], o[dt]);
+        const uint4 a = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) o[cg][dt] = mfma32x32x16<T>(a, pk[cg][k2], o[cg][dt]);
       }
     }
   };
@@ -272,19 +329,22 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_paged_kernel(
     }
   }
 
-  const float total = sum_xor32(lsum);
-  const float inv = total > 0.f ? 1.f / total : 0.f;  // a row that sees no key gives 0
-  if (row_ok) {
-    T* orow = out + (row * num_heads + head) * D;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int cg = 0; cg < CG; ++cg) {
+    const float total = sum_xor32(lsum[cg]);
+    const float inv = total > 0.f ? 1.f / total : 0.f;  // a row that sees no key gives 0
+    if (row_ok[cg]) {
+      T* orow = out + (row[cg] * num_heads + head[cg]) * D;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d0 = 32 * dt + 8 * i + 4 * half;
-        *reinterpret_cast<uint2*>(orow + d0) =
-            make_uint2(pack2<T>(o[dt][4 * i] * inv, o[dt][4 * i + 1] * inv),
-                       pack2<T>(o[dt][4 * i + 2] * inv, o[dt][4 * i + 3] * inv));
-      }
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = 32 * dt + 8 * i + 4 * half;
+          *reinterpret_cast<uint2*>(orow + d0) =
+              make_uint2(pack2<T>(o[cg][dt][4 * i] * inv, o[cg][dt][4 * i + 1] * inv),
+                         pack2<T>(o[cg][dt][4 * i + 2] * inv, o[cg][dt][4 * i + 3] * inv));
+        }
+    }
   }
 }
 
@@ -296,7 +356,7 @@ hipError_t launch_prefill_t(void* out, const void* query, const void* key_cache,
                             int32_t max_query_len, int32_t max_kv_len, int64_t total_query_rows,
                             float scale, int32_t causal, int32_t num_heads, const CacheGeom& g,
                             hipStream_t stream) {
-  constexpr int kPositions = 4 * (32 / G);
+  constexpr int kPositions = 4 * 32 * kPrefillColGroups / G;
   const int q_tiles = (max_query_len + kPositions - 1) / kPositions;
   const int64_t grid = (int64_t)num_seqs * q_tiles * g.num_kv_heads;
   if (grid == 0) return hipSuccess;
@@ -390,7 +450,7 @@ bool prefill_supported(int dtype, int head_dim, int block_size, int group) {
          (group == 1 || group == 2 || group == 4);
 }
 
-int prefill_positions_per_workgroup(int group) { return 4 * (32 / group); }
+int prefill_positions_per_workgroup(int group) { return 4 * 32 * kPrefillColGroups / group; }
 
 hipError_t launch_prefill_paged(int dtype, void* out, const void* query, const void* key_cache,
                                 const void* value_cache, const uint32_t* block_tables,

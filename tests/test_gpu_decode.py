@@ -109,6 +109,45 @@ def test_decode_config_c2(device):
     assert_attention_close(orc.to_f32(to_host(out), code), want, code, "c2")
 
 
+def test_decode_config_c3_layer(device):
+    """c3 at full size for one layer (bf16, B=256, contexts clip(Geom(1/800),
+    16, 4096), the layer's own shuffled pool of ~1.1 GB): the decode append
+    of 256 tokens is bit-exact over the whole pool (every other byte
+    unchanged), and attention over all 256 sequences matches the oracle on
+    a sample that includes the longest sequence and multi-chunk ones."""
+    from vpa import workloads
+    w = workloads.c3(num_layers=1)
+    layer = w.layers[0]
+    code = orc.BF16
+    g = torch.Generator(device=device)
+    g.manual_seed(w.seed)
+    kc_d = torch.randn((layer.num_blocks, 8, 16, 16, 8), generator=g, device=device,
+                       dtype=torch.bfloat16)
+    vc_d = torch.randn((layer.num_blocks, 8, 128, 16), generator=g, device=device,
+                       dtype=torch.bfloat16)
+    q_d = torch.randn((256, 16, 128), generator=g, device=device, dtype=torch.bfloat16)
+    nk_d = torch.randn((256, 8, 128), generator=g, device=device, dtype=torch.bfloat16)
+    nv_d = torch.randn((256, 8, 128), generator=g, device=device, dtype=torch.bfloat16)
+    kc, vc = to_host(kc_d), to_host(vc_d)
+    vpa.reshape_and_cache(nk_d, nv_d, None, None, kc_d, vc_d, i64(layer.slot_mapping, device))
+    out = vpa.paged_attention(q_d, None, None, kc_d, vc_d, u32(layer.block_tables, device),
+                              u32(w.context_lens, device), None, w.max_context_len,
+                              128 ** -0.5, 1.0, None)
+    torch.cuda.synchronize()
+    orc.reshape_and_cache(to_host(nk_d), to_host(nv_d), kc, vc, layer.slot_mapping, dtype=code)
+    assert np.array_equal(to_host(kc_d), kc)
+    assert np.array_equal(to_host(vc_d), vc)
+    lens = w.context_lens
+    sample = sorted({int(np.argmax(lens)), int(np.argmin(lens)),
+                     *np.nonzero(lens > 2048)[0][:4].tolist(),
+                     *np.nonzero((lens > 512) & (lens <= 1024))[0][:3].tolist(), 0, 1, 255})
+    q = to_host(q_d)[sample]
+    want = orc.paged_attention(q, kc, vc, layer.block_tables[sample], lens[sample],
+                               w.max_context_len, 128 ** -0.5, dtype=code)
+    got = orc.to_f32(to_host(out), code)[sample]
+    assert_attention_close(got, want, code, f"c3 sample {sample}")
+
+
 def test_decode_long_context_split_k(device):
     """Contexts spanning many split-K partitions (up to 8192 tokens)."""
     lens = [8192, 4097, 4096, 2049, 333]
