@@ -50,7 +50,58 @@ SIGNATURES = {
     "vpa_chunked_prefill_paged_attention": (ctypes.c_int, [
         _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i64, _f32, _i32, _i32,
         _i32, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
+    # include/vpa_host.h
+    "vpa_bytes_per_paged_block": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _p]),
+    "vpa_pool_blocks_for_context": (ctypes.c_int, [_i64, _i32, _p]),
+    "vpa_pool_blocks_for_byte_budget": (ctypes.c_int, [_u64, _u64, _p]),
+    "vpa_pool_blocks_for_memory_fraction": (ctypes.c_int, [_f32, _u64, _p]),
+    "vpa_block_manager_create": (ctypes.c_int, [_i64, _i32, _p]),
+    "vpa_block_manager_destroy": (None, [_p]),
+    "vpa_block_manager_free_blocks": (_i64, [_p]),
+    "vpa_block_manager_blocks_for_request": (_i64, [_p, _u64]),
+    "vpa_block_manager_total_allocated_blocks": (_i64, [_p]),
+    "vpa_block_manager_slots_available": (ctypes.c_int, [_p, _u64, _i64]),
+    "vpa_block_manager_try_allocate": (ctypes.c_int, [_p, _u64, _i64, _p]),
+    "vpa_block_manager_allocate": (ctypes.c_int, [_p, _u64, _i64]),
+    "vpa_block_manager_trim": (ctypes.c_int, [_p, _u64, _i64]),
+    "vpa_block_manager_free_request": (ctypes.c_int, [_p, _u64]),
+    "vpa_block_manager_block_ids": (ctypes.c_int, [_p, _u64, _p, _i64, _p]),
+    "vpa_block_manager_block_tables": (ctypes.c_int, [_p, _p, _i32, _i32, _p, _p]),
+    "vpa_slot_for_block_table_position": (ctypes.c_int, [_p, _i32, _i32, _i64, _i64, _p]),
+    "vpa_cumulative_seqlens": (ctypes.c_int, [_p, _i32, _p]),
+    "vpa_metadata_from_block_tables": (ctypes.c_int, [_p, _i32, _p, _i32, _p, _i32, _p, _i32,
+                                                      _i64, _p]),
+    "vpa_metadata_from_attention_masks": (ctypes.c_int, [_p, _i32, _p, _i32, _p, _i32, _i32,
+                                                         _i64, _p]),
+    "vpa_metadata_from_query_lens": (ctypes.c_int, [_p, _i32, _p, _i32, _p, _i32, _i64, _p]),
+    "vpa_decode_metadata_for_batch_steps": (ctypes.c_int, [_p, _i32, _p, _i32, _p, _i32, _i32,
+                                                           _i64, _i64, _i32, _i32, _p, _p, _p,
+                                                           _p]),
+    "vpa_contiguous_slot": (ctypes.c_int, [_i64, _i64, _i64, _i64, _i32, _i64, _p]),
+    "vpa_graph_batch_bucket": (_i32, [_i32, _i32]),
+    "vpa_graph_batch_buckets": (ctypes.c_int, [_i32, _p, _i32, _p]),
+    "vpa_bucket_block_table_cols": (_i64, [_i64, _i32]),
+    "vpa_pad_decode_batch": (ctypes.c_int, [_i32, _i32, _p, _p, _p, _p, _i32, _i32, _p, _p, _p,
+                                            _p]),
 }
+
+
+class PagedMetadata(ctypes.Structure):
+    """Mirror of vpa_paged_metadata (include/vpa_host.h)."""
+
+    _fields_ = [
+        ("slot_mapping", _p),
+        ("block_tables", _p),
+        ("context_lens", _p),
+        ("cu_seqlens_q", _p),
+        ("cu_seqlens_kv", _p),
+        ("cols", _i32),
+        ("num_tokens", _i64),
+        ("max_context_len", _i64),
+        ("max_query_len", _i64),
+        ("max_kv_len", _i64),
+        ("causal_only", _i32),
+    ]
 
 
 class VpaError(RuntimeError):
