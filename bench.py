@@ -10,11 +10,18 @@ lengths clip(Geom(mean 800), 16, 4096), every layer with its own pool and
 random block allocation. Inputs are synthetic (seeded) and resident in HBM
 before the timed region starts.
 
+The timed step is a HIP graph of the 28 layers replayed K times (vASR
+replays its decode step from a CUDA graph, vasr-paged-attn/src/cuda_graph.rs:
+204-225); `--eager` times eager launches instead. HIP events sit only at the
+two ends of each timed region.
+
 Prints one JSON line. `value` is the whole-step HBM throughput: algorithmic
 bytes of all appends and decodes of a step divided by the step time. The
-`roofline` object covers the dominant kernel (paged_attention, main + reduce
-launch) timed with HIP events on its stream; `cpu_baseline` times the
-oracle's restatement of the reference CPU path on a bounded sample.
+`roofline` object covers the dominant op (paged_attention: plan, rows and
+merge launches) timed back to back over the step's layers; `append_gbps`
+likewise for reshape_and_cache; `cpu_baseline` times the oracle's
+restatement of the reference CPU path on a bounded sample; `prefill_c4`
+reports the chunked-prefill row (append + MFMA prefill) on c4.
 """
 
 from __future__ import annotations
@@ -45,6 +52,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU baseline budget (0 disables it)")
     ap.add_argument("--seed", type=int, default=None)
+    ap.add_argument("--eager", action="store_true",
+                    help="time the step as eager launches instead of a HIP graph replay")
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="skip the c4 chunked-prefill measurement")
     return ap.parse_args()
@@ -92,20 +101,50 @@ def device_tensors(w, dev):
     return layers, ctx
 
 
-def run_step(layers, ctx, w, ws, ev=None):
+def decode_ops(layers, ctx, w, ws):
+    """Per layer: paged_attention over the layer's cache (thinker_text.rs:1126-1139)."""
     import vpa
 
     scale = w.head_dim ** -0.5
-    for i, L in enumerate(layers):
-        if ev is not None:
-            ev[i][0].record()
-        vpa.reshape_and_cache(L["k"], L["v"], None, None, L["kc"], L["vc"], L["slots"])
-        if ev is not None:
-            ev[i][1].record()
+    for L in layers:
         vpa.paged_attention(L["q"], None, None, L["kc"], L["vc"], L["bt"], ctx, None,
                             w.max_context_len, scale, 1.0, None, out=L["out"], workspace=ws)
-        if ev is not None:
-            ev[i][2].record()
+
+
+def append_ops(layers):
+    """Per layer: reshape_and_cache of the batch's new K/V (thinker_text.rs:1101-1109)."""
+    import vpa
+
+    for L in layers:
+        vpa.reshape_and_cache(L["k"], L["v"], None, None, L["kc"], L["vc"], L["slots"])
+
+
+def run_step(layers, ctx, w, ws):
+    """One decode step of the hot path: for each layer, append then attend."""
+    import vpa
+
+    scale = w.head_dim ** -0.5
+    for L in layers:
+        vpa.reshape_and_cache(L["k"], L["v"], None, None, L["kc"], L["vc"], L["slots"])
+        vpa.paged_attention(L["q"], None, None, L["kc"], L["vc"], L["bt"], ctx, None,
+                            w.max_context_len, scale, 1.0, None, out=L["out"], workspace=ws)
+
+
+def timed_ms(fn, reps):
+    """Milliseconds per call of fn over `reps` back-to-back calls: HIP events
+    on the current stream at the two ends of the region only, with a device
+    synchronisation on both sides."""
+    import torch
+
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def cpu_baseline(w, layers, budget_s):
@@ -245,32 +284,36 @@ def main():
         run_step(layers, ctx, w, ws)
     torch.cuda.synchronize()
 
-    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(nl)]
-          for _ in range(args.steps)]
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    # the step as vASR runs decode on the GPU: one HIP graph of the 28 layers
+    # (vasr-paged-attn/src/cuda_graph.rs:204-225), replayed; eager launches
+    # with --eager
+    step = lambda: run_step(layers, ctx, w, ws)  # noqa: E731
+    execution = "eager launches"
+    if not args.eager:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run_step(layers, ctx, w, ws)
+        torch.cuda.synchronize()
+        step = graph.replay
+        execution = "hip graph replay of the whole step"
+        for _ in range(args.warmup):
+            step()
     wall0 = time.perf_counter()
-    t_start.record()
-    for s in range(args.steps):
-        run_step(layers, ctx, w, ws, ev[s])
-    t_end.record()
-    torch.cuda.synchronize()
+    ms_per_step = timed_ms(step, args.steps)
     wall = time.perf_counter() - wall0
 
-    gpu_ms = t_start.elapsed_time(t_end)
-    ms_per_step = gpu_ms / args.steps
-    append_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1])
-                    for s in range(args.steps) for i in range(nl))
-    decode_ms = sum(ev[s][i][1].elapsed_time(ev[s][i][2])
-                    for s in range(args.steps) for i in range(nl))
-    launches = args.steps * nl
+    # the two ops on their own, back to back over the same layers (the
+    # per-op figures and the roofline), and the eager step for comparison
+    eager_ms = timed_ms(lambda: run_step(layers, ctx, w, ws), args.steps)
+    decode_ms = timed_ms(lambda: decode_ops(layers, ctx, w, ws), args.steps)
+    append_ms = timed_ms(lambda: append_ops(layers), args.steps)
+
     dec_bytes = w.decode_bytes_per_layer()
     app_bytes = w.append_bytes_per_layer()
     step_bytes = nl * (dec_bytes + app_bytes)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    dec_launch_ms = decode_ms / launches
-    app_launch_ms = append_ms / launches
+    dec_launch_ms = decode_ms / nl
+    app_launch_ms = append_ms / nl
     dec_gbps = dec_bytes / (dec_launch_ms * 1e-3) / 1e9
     app_gbps = app_bytes / (app_launch_ms * 1e-3) / 1e9
 
@@ -304,6 +347,7 @@ def main():
         "data": "synthetic (seeded)",
         "config": {
             "workload": w.name,
+            "execution": execution,
             "num_seqs": w.num_seqs,
             "layers": nl,
             "q_heads": w.num_heads,
@@ -314,13 +358,16 @@ def main():
             "max_context_len": w.max_context_len,
             "seed": w.seed,
         },
+        "eager_ms_per_step": round(eager_ms, 4),
+        "eager_value": round(step_bytes / (eager_ms * 1e-3) / 1e9, 2),
         "decode_gbps": round(dec_gbps, 2),
         "decode_frac_of_peak": round(dec_gbps / HBM_PEAK_GBPS, 4),
         "append_gbps": round(app_gbps, 2),
         "append_us_per_launch": round(app_launch_ms * 1e3, 2),
         "wall_s_timed_region": round(wall, 4),
         "roofline": {
-            "kernel": "paged_attention (decode main + split-K reduce)",
+            "kernel": "paged_attention (plan + rows + merge launches), back to back over "
+                      "the step's layers",
             "bound": "hbm",
             "achieved": round(dec_gbps, 2),
             "peak": HBM_PEAK_GBPS,

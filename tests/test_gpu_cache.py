@@ -69,6 +69,43 @@ def test_append_padding_and_out_of_range_slots(device):
     run_append(device, orc.BF16, 8, 128, bs, nb, np.full(16, -1, dtype=np.int64), seed=5)
 
 
+def test_append_small_call_mixes_lone_and_shared_blocks(device):
+    """Tokens alone in their block next to tokens sharing a block with
+    another token of the same call (and of the same 16-token group)."""
+    nb, bs = 32, 16
+    slots = np.array([3 * bs + 0, 3 * bs + 5, 7 * bs + 2, 9 * bs + 15, 9 * bs + 14, 11 * bs + 8,
+                      -1, 12 * bs + 1, 31 * bs + 15], dtype=np.int64)
+    for code in (orc.BF16, orc.F32):
+        run_append(device, code, 8, 128, bs, nb, slots, seed=21 + code)
+    # scattered single tokens at two sizes
+    rng = np.random.default_rng(22)
+    for t in (1024, 1025):
+        nb2 = 2048
+        run_append(device, orc.BF16, 2, 64, bs, nb2, rng.choice(nb2 * bs, size=t, replace=False),
+                   seed=23)
+
+
+def test_append_large_mixed_call(device):
+    """A large call: aligned whole blocks, ragged heads and tails, padding
+    and out-of-pool slots."""
+    rng = np.random.default_rng(24)
+    nb, kvh, d, bs = 400, 4, 128, 16
+    prior = [0, 7, 16, 40, 3]
+    new = [512, 300, 257, 200, 33]
+    lens = [p + n for p, n in zip(prior, new)]
+    bt = block_tables_for(rng, lens, nb, bs)
+    slots = []
+    for s, (p, n) in enumerate(zip(prior, new)):
+        pos = np.arange(p, p + n)
+        slots.append(bt[s, pos // bs].astype(np.int64) * bs + pos % bs)
+    slots = np.concatenate(slots)
+    slots[100:116] = -1
+    slots[700] = nb * bs + 3
+    assert len(slots) > 1024
+    for code in (orc.BF16, orc.F32):
+        run_append(device, code, kvh, d, bs, nb, slots, seed=25 + code)
+
+
 def test_append_config_c1_prefill_then_append(device):
     """c1: 511 prefilled positions then one append at 511 into 32 blocks of a
     64-block pool, f32, 8 kv heads x 128."""
