@@ -389,9 +389,10 @@ void paged_decode_rows_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const uint32_t w = blockIdx.x;
-  if (w >= queue[1] * (uint32_t)num_kv_heads) return;  // surplus workgroup of the grid
-  const uint2 item = items[w / (uint32_t)num_kv_heads];
   const int j = (int)(w % (uint32_t)num_kv_heads);
+  const uint32_t want = w / (uint32_t)num_kv_heads;  // index of this workgroup's item
+  if (want >= queue[1]) return;  // surplus workgroup of the grid
+  const uint2 item = items[want];
   const int s = (int)(item.x >> 16);
   const int chunk = (int)(item.x & 0xffffu);
   const int L = (int)item.y;
@@ -673,74 +674,72 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
 #define VPA_DECODE_ROWS_PT 128
 #endif
 #ifndef VPA_DECODE_ROWS_WAVES
-#define VPA_DECODE_ROWS_WAVES 4
+#define VPA_DECODE_ROWS_WAVES 8
 #endif
 constexpr int kRowsPT = VPA_DECODE_ROWS_PT;  // partition tokens per wave of the rows kernel
 constexpr int kRowsWaves = VPA_DECODE_ROWS_WAVES;  // waves (partitions) per workgroup
 static_assert(kRowsPT >= kDecodeMinPartitionTokens, "workspace sized for 128-token partitions");
 
-// Merge of split-K partials: persistent waves over (multi-partition
-// sequence from the plan, query head) units.
+// Merge of split-K partials: persistent waves over (sequence, query head)
+// units; sequences of one chunk were written directly and are skipped. One
+// pass with an online max: each step loads the stats and the rows of up to
+// kMergeRows partials together, so a unit costs two dependent loads
+// (the context length, then its partials) before the store.
+constexpr int kMergeRows = 8;
+
 template <typename T, int D>
 __global__ __launch_bounds__(64) void decode_merge_kernel(
-    T* __restrict__ out, const uint32_t* __restrict__ context_lens, int32_t max_ctx,
-    int32_t cap_tokens, int32_t part_tokens, int32_t num_heads, const float* __restrict__ part,
-    int32_t max_parts, const uint32_t* __restrict__ multi, const uint32_t* __restrict__ queue) {
+    T* __restrict__ out, const uint32_t* __restrict__ context_lens, int32_t num_seqs,
+    int32_t max_ctx, int32_t cap_tokens, int32_t part_tokens, int32_t num_heads,
+    const float* __restrict__ part, int32_t max_parts) {
   constexpr int DPL = D / 64;
   constexpr int RS = kPartRow<D>;
-  __shared__ float s_w[64];
+  constexpr int R = kMergeRows;
   const int lane = threadIdx.x;
-  const uint32_t units = queue[2] * (uint32_t)num_heads;
+  const uint32_t units = (uint32_t)num_seqs * (uint32_t)num_heads;
   for (uint32_t u = blockIdx.x; u < units; u += gridDim.x) {
-    const int s = (int)multi[u / (uint32_t)num_heads];
+    const int s = (int)(u / (uint32_t)num_heads);
     const int h = (int)(u % (uint32_t)num_heads);
     const int L = clamp_context(context_lens[s], max_ctx, cap_tokens);
     const int nparts = (L + part_tokens - 1) / part_tokens;
+    if (nparts <= 1) continue;
     const float* rows = part + ((int64_t)s * num_heads + h) * max_parts * RS;
-    float mx = -INFINITY;
-    for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, rows[(int64_t)p * RS + D]);
-    mx = wave_max_dpp(mx);
-    float tot = 0.f;
+    float mx = -INFINITY, tot = 0.f;
     float a[DPL];
 #pragma unroll
     for (int k = 0; k < DPL; ++k) a[k] = 0.f;
-    for (int c0 = 0; c0 < nparts; c0 += 64) {
-      const int p = c0 + lane;
-      float wgt = 0.f;
-      if (p < nparts) {
-        const float pm = rows[(int64_t)p * RS + D];
-        wgt = pm == -INFINITY ? 0.f : expf(pm - mx);
-        tot += wgt * rows[(int64_t)p * RS + D + 1];
+    for (int c0 = 0; c0 < nparts; c0 += R) {
+      const int cn = min(R, nparts - c0);
+      float pm[R], pl[R], v[R][DPL];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float* row = rows + (int64_t)(c0 + min(r, cn - 1)) * RS;
+        pm[r] = r < cn ? row[D] : -INFINITY;
+        pl[r] = row[D + 1];
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) v[r][k] = row[lane + 64 * k];
       }
-      lds_wave_sync();
-      s_w[lane] = wgt;
-      lds_wave_sync();
-      const int cn = min(64, nparts - c0);
-      int q = 0;
-      // four partial rows in flight per step
-      for (; q + 4 <= cn; q += 4) {
-        float v[4][DPL];
+      float cm = mx;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < R; ++r) cm = fmaxf(cm, pm[r]);
+      if (cm == -INFINITY) continue;  // no token in these partials
+      const float rescale = mx == -INFINITY ? 0.f : expf(mx - cm);
+      tot *= rescale;
 #pragma unroll
-          for (int k = 0; k < DPL; ++k) v[r][k] = rows[(int64_t)(c0 + q + r) * RS + lane + 64 * k];
+      for (int k = 0; k < DPL; ++k) a[k] *= rescale;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < R; ++r) {
+        const float wgt = pm[r] == -INFINITY ? 0.f : expf(pm[r] - cm);
+        tot = fmaf(wgt, pl[r], tot);
 #pragma unroll
-          for (int k = 0; k < DPL; ++k) a[k] = fmaf(s_w[q + r], v[r][k], a[k]);
+        for (int k = 0; k < DPL; ++k) a[k] = fmaf(wgt, v[r][k], a[k]);
       }
-      for (; q < cn; ++q) {
-#pragma unroll
-        for (int k = 0; k < DPL; ++k)
-          a[k] = fmaf(s_w[q], rows[(int64_t)(c0 + q) * RS + lane + 64 * k], a[k]);
-      }
+      mx = cm;
     }
-    tot = wave_sum_dpp(tot);
     const float inv = 1.f / (tot + 1e-6f);
     T* orow = out + ((int64_t)s * num_heads + h) * D + lane;
 #pragma unroll
     for (int k = 0; k < DPL; ++k) store_from_f32<T>(orow + 64 * k, a[k] * inv);
-    lds_wave_sync();
   }
 }
 
@@ -768,8 +767,8 @@ hipError_t launch_decode_rows(void* out, const void* q, const void* kc, const vo
   const int64_t munits = (int64_t)num_seqs * num_heads;
   const int64_t mwaves = std::min<int64_t>(munits, (int64_t)device_cu_count() * 8);
   hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)mwaves), dim3(64), 0, stream,
-                     static_cast<T*>(out), cl, max_ctx, cap_tokens, kChunk, num_heads,
-                     ws.part_out, ws.max_parts, ws.multi, ws.queue);
+                     static_cast<T*>(out), cl, num_seqs, max_ctx, cap_tokens, kChunk, num_heads,
+                     ws.part_out, ws.max_parts);
   return hipGetLastError();
 }
 
