@@ -144,6 +144,45 @@ int vpa_paged_attention(void* out, const void* query, const float* k_scale,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * paged_attention_plan — build the decode work list of one step into
+ * `workspace` once, for the paged_attention calls of every layer of that
+ * step (vASR calls paged_attention once per decoder layer with the same
+ * block tables and context lengths, thinker_text.rs:1126-1139, so the list
+ * is per-step metadata like them). Arguments mean what they mean in
+ * vpa_paged_attention; the workspace is that call's. Stream-ordered and
+ * capture-safe; a no-op for configurations whose kernel needs no list.
+ * No counterpart in the reference (its decode kernel sizes its grid from
+ * max_context_len only).
+ */
+int vpa_paged_attention_plan(const uint32_t* context_lens, int32_t max_context_len,
+                             int32_t block_table_stride, int32_t num_seqs, int32_t num_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                             int32_t dtype, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/*
+ * paged_attention_planned — vpa_paged_attention without the work-list
+ * launch: `workspace` must hold the list that vpa_paged_attention_plan built
+ * from the same context_lens contents, max_context_len, block_table_stride,
+ * num_seqs and head configuration, earlier in stream order (and no other
+ * paged_attention call on that workspace in between). Same arguments,
+ * results and errors as vpa_paged_attention. A list that does not match
+ * gives wrong results but every memory access stays inside the arguments'
+ * bounds.
+ */
+int vpa_paged_attention_planned(void* out, const void* query, const float* k_scale,
+                                const float* v_scale, const void* key_cache,
+                                const void* value_cache, const uint32_t* block_tables,
+                                int32_t block_table_stride, const uint32_t* context_lens,
+                                const float* alibi_slopes, int32_t max_context_len,
+                                float softmax_scale, float softcapping, const float* sinks,
+                                int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                int64_t cache_block_stride, int64_t cache_head_stride,
+                                int32_t dtype, int32_t cache_dtype, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/*
  * gather_kv_cache — copy each sequence's first kv_len tokens out of the paged
  * cache into packed rows.
  * Replaces mistralrs_paged_attn::gather_kv_cache(key_cache, value_cache,

@@ -213,20 +213,22 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
   return decode_workspace_bytes(num_seqs, num_heads, head_dim, max_context_len);
 }
 
-int vpa_paged_attention(void* out, const void* query, const float* k_scale,
-                        const float* v_scale, const void* key_cache, const void* value_cache,
-                        const uint32_t* block_tables, int32_t block_table_stride,
-                        const uint32_t* context_lens, const float* alibi_slopes,
-                        int32_t max_context_len, float softmax_scale, float softcapping,
-                        const float* sinks, int32_t num_seqs, int32_t num_heads,
-                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                        int64_t num_blocks, int64_t cache_block_stride,
-                        int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
-                        void* workspace, size_t workspace_bytes, void* stream) {
-  (void)k_scale;
-  (void)v_scale;
+}  // extern "C"
+
+namespace {
+
+// paged_attention and its planned variant: all checks, then the launch.
+int paged_attention_impl(void* out, const void* query, const void* key_cache,
+                         const void* value_cache, const uint32_t* block_tables,
+                         int32_t block_table_stride, const uint32_t* context_lens,
+                         const float* alibi_slopes, int32_t max_context_len, float softmax_scale,
+                         float softcapping, const float* sinks, int32_t num_seqs,
+                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                         int32_t block_size, int64_t num_blocks, int64_t cache_block_stride,
+                         int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
+                         void* workspace, size_t workspace_bytes, void* stream, bool planned) {
   clear_error();
-  const char* op = "paged_attention";
+  const char* op = planned ? "paged_attention_planned" : "paged_attention";
   if (alibi_slopes != nullptr)
     return fail(VPA_ERR_UNSUPPORTED, "%s: alibi_slopes are not supported", op);
   if (sinks != nullptr) return fail(VPA_ERR_UNSUPPORTED, "%s: sinks are not supported", op);
@@ -258,8 +260,8 @@ int vpa_paged_attention(void* out, const void* query, const float* k_scale,
   if (num_seqs > 65535)
     return fail(VPA_ERR_UNSUPPORTED, "%s: num_seqs=%d exceeds 65535", op, num_seqs);
   {
-    // one wavefront per (sequence, partition, kv head): keep the 1-D grid
-    // below 2^25 workgroups
+    // one workgroup per (sequence, partition, kv head) at most: keep the
+    // 1-D grid below 2^25 workgroups
     const int64_t parts =
         std::max<int64_t>(1, ((int64_t)max_context_len + kDecodeMinPartitionTokens - 1) /
                                  kDecodeMinPartitionTokens);
@@ -289,10 +291,98 @@ int vpa_paged_attention(void* out, const void* query, const float* k_scale,
               cache_head_stride};
   DecodeWorkspace ws =
       carve_decode_workspace(workspace, num_seqs, num_heads, head_dim, max_context_len);
+  ws.planned = planned;
   return hip_status(op, launch_paged_decode(dtype, out, query, key_cache, value_cache,
                                             block_tables, block_table_stride, context_lens,
                                             max_context_len, softmax_scale, num_seqs, num_heads,
                                             g, ws, static_cast<hipStream_t>(stream)));
+}
+
+}  // namespace
+
+extern "C" {
+
+int vpa_paged_attention(void* out, const void* query, const float* k_scale,
+                        const float* v_scale, const void* key_cache, const void* value_cache,
+                        const uint32_t* block_tables, int32_t block_table_stride,
+                        const uint32_t* context_lens, const float* alibi_slopes,
+                        int32_t max_context_len, float softmax_scale, float softcapping,
+                        const float* sinks, int32_t num_seqs, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int64_t num_blocks, int64_t cache_block_stride,
+                        int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  (void)k_scale;
+  (void)v_scale;
+  return paged_attention_impl(out, query, key_cache, value_cache, block_tables,
+                              block_table_stride, context_lens, alibi_slopes, max_context_len,
+                              softmax_scale, softcapping, sinks, num_seqs, num_heads,
+                              num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
+                              cache_head_stride, dtype, cache_dtype, workspace, workspace_bytes,
+                              stream, false);
+}
+
+int vpa_paged_attention_planned(void* out, const void* query, const float* k_scale,
+                                const float* v_scale, const void* key_cache,
+                                const void* value_cache, const uint32_t* block_tables,
+                                int32_t block_table_stride, const uint32_t* context_lens,
+                                const float* alibi_slopes, int32_t max_context_len,
+                                float softmax_scale, float softcapping, const float* sinks,
+                                int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                int64_t cache_block_stride, int64_t cache_head_stride,
+                                int32_t dtype, int32_t cache_dtype, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  (void)k_scale;
+  (void)v_scale;
+  return paged_attention_impl(out, query, key_cache, value_cache, block_tables,
+                              block_table_stride, context_lens, alibi_slopes, max_context_len,
+                              softmax_scale, softcapping, sinks, num_seqs, num_heads,
+                              num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
+                              cache_head_stride, dtype, cache_dtype, workspace, workspace_bytes,
+                              stream, true);
+}
+
+int vpa_paged_attention_plan(const uint32_t* context_lens, int32_t max_context_len,
+                             int32_t block_table_stride, int32_t num_seqs, int32_t num_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                             int32_t dtype, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  clear_error();
+  const char* op = "paged_attention_plan";
+  if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+      max_context_len < 0 || block_table_stride < 0 || num_heads % num_kv_heads != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: bad sizes num_seqs=%d num_heads=%d num_kv_heads=%d head_dim=%d "
+                "block_size=%d max_context_len=%d block_table_stride=%d",
+                op, num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_context_len,
+                block_table_stride);
+  if (!decode_supported(dtype, head_dim, block_size, num_heads / num_kv_heads))
+    return fail(VPA_ERR_UNSUPPORTED, "%s: no decode kernel for this configuration", op);
+  if (max_context_len > kDecodeMaxPartitions * kDecodeMinPartitionTokens)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: max_context_len=%d exceeds %d", op, max_context_len,
+                kDecodeMaxPartitions * kDecodeMinPartitionTokens);
+  if (num_seqs == 0) return VPA_OK;
+  if (num_seqs > 65535)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: num_seqs=%d exceeds 65535", op, num_seqs);
+  if (context_lens == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: context_lens must be non-null", op);
+  if (max_context_len > 0 && (int64_t)block_table_stride * block_size < max_context_len)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: block_table_stride=%d too small for max_context_len=%d (block_size=%d)", op,
+                block_table_stride, max_context_len, block_size);
+  const size_t need = decode_workspace_bytes(num_seqs, num_heads, head_dim, max_context_len);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(VPA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", op, need,
+                workspace == nullptr ? (size_t)0 : workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned", op);
+  CacheGeom g{num_kv_heads, head_dim, block_size, 1, 0, 0};
+  DecodeWorkspace ws =
+      carve_decode_workspace(workspace, num_seqs, num_heads, head_dim, max_context_len);
+  return hip_status(op, launch_decode_plan(dtype, context_lens, max_context_len,
+                                           block_table_stride, num_seqs, g, ws,
+                                           static_cast<hipStream_t>(stream)));
 }
 
 int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,

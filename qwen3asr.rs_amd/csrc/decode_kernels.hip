@@ -359,7 +359,8 @@ void paged_decode_rows_kernel(
     const T* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
     int32_t block_table_stride, float scale, int32_t num_heads, int32_t num_kv_heads,
     int64_t num_blocks, int64_t block_stride, int64_t head_stride, float* __restrict__ part_out,
-    int32_t max_parts, const uint2* __restrict__ items, const uint32_t* __restrict__ queue) {
+    int32_t max_parts, const uint2* __restrict__ items, const uint32_t* __restrict__ queue,
+    int32_t num_seqs, int32_t max_ctx, int32_t cap_tokens) {
   constexpr int X = pack_x<T>();
   static_assert(X == 8, "16-bit element types only");
   constexpr int PB = PT / BS;        // blocks per wave partition
@@ -395,7 +396,10 @@ void paged_decode_rows_kernel(
   const uint2 item = items[want];
   const int s = (int)(item.x >> 16);
   const int chunk = (int)(item.x & 0xffffu);
-  const int L = (int)item.y;
+  // a work list built by an earlier call is only trusted within this call's
+  // bounds (sequence index, context cap), so every access stays in range
+  if (s >= num_seqs) return;
+  const int L = clamp_context(item.y, max_ctx, cap_tokens);
   if (L <= 0) {
     for (int i = threadIdx.x; i < G * D; i += 64 * NW)
       store_from_f32<T>(out + ((int64_t)s * num_heads + j * G) * D + i, 0.f);
@@ -750,10 +754,13 @@ hipError_t launch_decode_rows(void* out, const void* q, const void* kc, const vo
                               const CacheGeom& g, const DecodeWorkspace& ws, hipStream_t stream) {
   constexpr int kChunk = kRowsPT * kRowsWaves;  // tokens per workgroup
   const int cap_tokens = bts * g.block_size;
-  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, cl, num_seqs, max_ctx,
-                     cap_tokens, kChunk, ws.items, ws.multi, ws.queue);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  hipError_t e = hipSuccess;
+  if (!ws.planned) {
+    hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, cl, num_seqs,
+                       max_ctx, cap_tokens, kChunk, ws.items, ws.multi, ws.queue);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   const int max_chunks = max(1, (max_ctx + kChunk - 1) / kChunk);
   const int64_t units = (int64_t)num_seqs * max_chunks * g.num_kv_heads;
   hipLaunchKernelGGL((paged_decode_rows_kernel<T, D, BS, G, kRowsPT, kRowsWaves>),
@@ -761,7 +768,7 @@ hipError_t launch_decode_rows(void* out, const void* q, const void* kc, const vo
                      static_cast<T*>(out), static_cast<const T*>(q), static_cast<const T*>(kc),
                      static_cast<const T*>(vc), bt, bts, scale, num_heads, g.num_kv_heads,
                      g.num_blocks, g.block_stride, g.head_stride, ws.part_out, ws.max_parts,
-                     ws.items, ws.queue);
+                     ws.items, ws.queue, num_seqs, max_ctx, cap_tokens);
   e = hipGetLastError();
   if (e != hipSuccess || max_chunks <= 1) return e;
   const int64_t munits = (int64_t)num_seqs * num_heads;
@@ -836,6 +843,17 @@ hipError_t dispatch_decode(int dtype, int D, int BS, int group, A... args) {
 }
 
 }  // namespace
+
+hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t max_context_len,
+                              int32_t block_table_stride, int32_t num_seqs, const CacheGeom& g,
+                              const DecodeWorkspace& ws, hipStream_t stream) {
+  const bool rows = (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) && g.head_dim <= 128;
+  if (!rows || num_seqs == 0) return hipSuccess;
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, context_lens, num_seqs,
+                     max_context_len, block_table_stride * g.block_size, kRowsPT * kRowsWaves,
+                     ws.items, ws.multi, ws.queue);
+  return hipGetLastError();
+}
 
 bool decode_supported(int dtype, int head_dim, int block_size, int group) {
   return cache_kernels_supported(dtype, head_dim, block_size) &&

@@ -42,6 +42,7 @@ struct DecodeWorkspace {
   uint32_t* multi;   // [num_seqs] sequences with more than one partition
   uint32_t* queue;   // [3]: next work unit, number of items, number of multi entries
   int max_parts;     // ceil(max_context_len / kDecodeMinPartitionTokens)
+  bool planned = false;  // the work list is already in the workspace (skip the plan launch)
 };
 
 // Compute units of the current device (cached per device).
@@ -84,6 +85,13 @@ hipError_t launch_prefill_paged(int dtype, void* out, const void* query, const v
 int prefill_positions_per_workgroup(int group);
 // True when the MFMA prefill kernel is compiled for this combination.
 bool prefill_supported(int dtype, int head_dim, int block_size, int group);
+
+// Builds the decode work list into the workspace (the plan launch of
+// launch_paged_decode on its own); a no-op for configurations whose decode
+// kernel takes no work list.
+hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t max_context_len,
+                              int32_t block_table_stride, int32_t num_seqs, const CacheGeom& g,
+                              const DecodeWorkspace& ws, hipStream_t stream);
 
 // True when a decode kernel is compiled for this (dtype, head_dim, block_size,
 // query heads per kv head) combination.

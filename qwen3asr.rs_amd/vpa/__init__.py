@@ -10,6 +10,7 @@ from .ops import (  # noqa: F401
     cache_geometry,
     gather_kv_cache,
     paged_attention,
+    paged_attention_plan,
     paged_attention_varlen_prefill,
     paged_attention_workspace,
     reshape_and_cache,
@@ -20,6 +21,7 @@ __all__ = [
     "cache_geometry",
     "gather_kv_cache",
     "paged_attention",
+    "paged_attention_plan",
     "paged_attention_varlen_prefill",
     "paged_attention_workspace",
     "reshape_and_cache",

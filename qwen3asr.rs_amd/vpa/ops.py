@@ -147,12 +147,15 @@ def paged_attention(q: torch.Tensor, k_scale: Optional[torch.Tensor],
                     context_lens: torch.Tensor, alibi_slopes: Optional[torch.Tensor],
                     max_context_len: int, softmax_scale: float, softcapping: float,
                     sinks: Optional[torch.Tensor], *, out: Optional[torch.Tensor] = None,
-                    workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    workspace: Optional[torch.Tensor] = None,
+                    planned: bool = False) -> torch.Tensor:
     """Single-token decode attention over the paged cache; returns [B, H, D].
 
     ``out`` and ``workspace`` are optional pre-allocated buffers (for callers
     that capture the call in a HIP graph); otherwise they are allocated from
-    torch's caching allocator."""
+    torch's caching allocator. ``planned=True`` uses the work list that
+    ``paged_attention_plan`` wrote into ``workspace`` for this step's
+    context lengths instead of building it again."""
     _require_device(q, key_cache, value_cache, block_tables, context_lens)
     nb, kvh, d, bs, bstride, hstride = cache_geometry(key_cache, value_cache)
     if q.dim() != 3 or q.shape[2] != d:
@@ -176,7 +179,10 @@ def paged_attention(q: torch.Tensor, k_scale: Optional[torch.Tensor],
     if workspace is None and need > 0:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    check(lib.vpa_paged_attention(
+    if planned and workspace is None:
+        raise _err("planned=True needs the workspace paged_attention_plan filled")
+    fn = lib.vpa_paged_attention_planned if planned else lib.vpa_paged_attention
+    check(fn(
         out.data_ptr(), q.data_ptr(), _ptr(k_scale), _ptr(v_scale), key_cache.data_ptr(),
         value_cache.data_ptr(), block_tables.data_ptr(), block_tables.shape[1],
         context_lens.data_ptr(), _ptr(alibi_slopes), int(max_context_len), float(softmax_scale),
@@ -184,6 +190,22 @@ def paged_attention(q: torch.Tensor, k_scale: Optional[torch.Tensor],
         dtype_code(q.dtype), dtype_code(key_cache.dtype), _ptr(workspace), ws_bytes,
         _stream(q)))
     return out
+
+
+def paged_attention_plan(context_lens: torch.Tensor, max_context_len: int,
+                         block_table_stride: int, num_heads: int, key_cache: torch.Tensor,
+                         value_cache: torch.Tensor, dtype: torch.dtype,
+                         workspace: torch.Tensor) -> None:
+    """Build one step's decode work list into ``workspace`` (shared by the
+    ``paged_attention(..., planned=True)`` calls of all layers of the step)."""
+    _require_device(context_lens, workspace)
+    nb, kvh, d, bs, _, _ = cache_geometry(key_cache, value_cache)
+    if context_lens.dtype != torch.uint32 or context_lens.dim() != 1:
+        raise _err(f"context_lens must be u32 1-d, got {context_lens.dtype}")
+    check(_lib.load().vpa_paged_attention_plan(
+        context_lens.contiguous().data_ptr(), int(max_context_len), int(block_table_stride),
+        context_lens.shape[0], num_heads, kvh, d, bs, dtype_code(dtype), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream(context_lens)))
 
 
 def gather_kv_cache(key_cache: torch.Tensor, value_cache: torch.Tensor,

@@ -201,3 +201,45 @@ def test_prefill_empty_is_noop():
     assert pf_call(b=0, out=None, q=None)[0] == 0
     assert pf_call(maxq=0)[0] == 0
     assert pf_call(tq=0)[0] == 0
+
+
+def plan_call(**over):
+    args = dict(cl=FAKE, max_ctx=1024, bts=64, b=4, h=16, kvh=8, d=128, bs=16,
+                dtype=_lib.DTYPE_BF16, ws=FAKE * 256, ws_bytes=1 << 30, stream=None)
+    args.update(over)
+    lib = _lib.load()
+    rc = lib.vpa_paged_attention_plan(*args.values())
+    return rc, lib.vpa_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,needle", [
+    (dict(ws=None), _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(ws_bytes=16), _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(ws=FAKE * 256 + 16), _lib.VPA_ERR_INVALID_ARGUMENT, "256-byte"),
+    (dict(h=12), _lib.VPA_ERR_INVALID_ARGUMENT, "bad sizes"),
+    (dict(h=64), _lib.VPA_ERR_UNSUPPORTED, "no decode kernel"),
+    (dict(cl=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
+    (dict(bts=10), _lib.VPA_ERR_INVALID_ARGUMENT, "block_table_stride"),
+    (dict(b=70000), _lib.VPA_ERR_UNSUPPORTED, "num_seqs"),
+])
+def test_paged_attention_plan_host_validation(over, code, needle):
+    rc, msg = plan_call(**over)
+    assert rc == code, msg
+    assert needle in msg
+
+
+def test_paged_attention_planned_validates_like_paged_attention():
+    lib = _lib.load()
+    for over in (dict(alibi=FAKE), dict(softcap=2.0), dict(), dict(h=12)):
+        args = dict(out=FAKE, q=FAKE, ks=None, vs=None, kc=FAKE, vc=FAKE, bt=FAKE, bts=64, cl=FAKE,
+                    alibi=None, max_ctx=1024, scale=0.088, softcap=1.0, sinks=None, b=4, h=16,
+                    kvh=8, d=128, bs=16, nb=100, bstride=8 * 128 * 16, hstride=128 * 16,
+                    dtype=_lib.DTYPE_BF16, cdtype=_lib.DTYPE_BF16, ws=None, ws_bytes=0,
+                    stream=None)
+        args.update(over)
+        rc_a = lib.vpa_paged_attention(*args.values())
+        msg_a = lib.vpa_last_error().decode()
+        rc_b = lib.vpa_paged_attention_planned(*args.values())
+        msg_b = lib.vpa_last_error().decode()
+        assert rc_a == rc_b != 0
+        assert msg_b.replace("paged_attention_planned", "paged_attention") == msg_a

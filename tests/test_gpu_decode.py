@@ -254,3 +254,33 @@ def test_decode_preallocated_out_and_workspace(device):
                             u32(bt, device), u32(lens, device), None, 900, 0.088, 1.0, None,
                             workspace=ws[:100])
     assert e.value.code == 3
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F32])
+def test_decode_planned_layers_match_unplanned(device, code):
+    """One work list per step shared by several layers (paged_attention_plan
+    + paged_attention(planned=True)) gives bit-identical outputs to building
+    it in every call; for f32 (no work list) the plan is a no-op."""
+    rng = np.random.default_rng(61 + code)
+    h, kvh, d, bs = 16, 8, 128, 16
+    lens = np.asarray([1, 16, 300, 1024, 1025, 2049, 77, 4000], dtype=np.uint32)
+    max_ctx = 4096
+    nb = int(sum((int(L) + bs - 1) // bs for L in lens)) + 4
+    bt = block_tables_for(rng, lens, nb, bs, pad_cols=8)
+    ctx = u32(lens, device)
+    bt_d = u32(bt, device)
+    ws = vpa.paged_attention_workspace(len(lens), h, d, max_ctx, device)
+    dt = {orc.BF16: torch.bfloat16, orc.F32: torch.float32}[code]
+    layers = []
+    for _ in range(3):
+        kc, vc = make_cache(rng, nb, kvh, d, bs, code)
+        q = random_words(rng, (len(lens), h, d), code)
+        layers.append((to_dev(q, code, device), to_dev(kc, code, device), to_dev(vc, code, device)))
+    want = [vpa.paged_attention(q, None, None, kc, vc, bt_d, ctx, None, max_ctx, d ** -0.5, 1.0,
+                                None) for q, kc, vc in layers]
+    vpa.paged_attention_plan(ctx, max_ctx, bt.shape[1], h, layers[0][1], layers[0][2], dt, ws)
+    got = [vpa.paged_attention(q, None, None, kc, vc, bt_d, ctx, None, max_ctx, d ** -0.5, 1.0,
+                               None, workspace=ws, planned=True) for q, kc, vc in layers]
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert torch.equal(a, b), f"layer {i}"
