@@ -27,6 +27,23 @@
 // 16-key step for lane half h). The probabilities are rounded to the cache
 // type for the MFMA; the row sums use the unrounded values. The output is
 // acc / sum without an epsilon, as flash attention computes it.
+//
+// Tile pipeline: K and V tiles travel HBM -> LDS by the LDS-DMA form of the
+// 16-byte global load (no VGPR round trip) into kPrefillStages stage
+// buffers; tile t + stages - 1 is issued while tile t is consumed, waits are
+// explicit vmcnt counts plus a bare workgroup barrier (the compiler's
+// __syncthreads would drain every outstanding DMA), and the operand reads
+// from LDS are written as ds_read with their own lgkmcnt wait so the
+// compiler does not add a full vmcnt drain before them. V is stored [dim]
+// [key] with its 16-byte units XOR-swizzled by dim to spread the banks.
+//
+// Softmax: scores are in log2 units (scale * log2 e folded into the scale);
+// the running max only moves when a tile's max exceeds it by more than
+// kRescaleSlack, so O and the row sums are rescaled rarely and the
+// probabilities stay below 2^kRescaleSlack; the result is the same
+// sum(p v) / sum(p) for any choice of the reference max.
+#include <type_traits>
+
 #include "vpa_device.h"
 #include "vpa_internal.h"
 
@@ -61,18 +78,67 @@ __device__ __forceinline__ float max_xor32(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-#ifndef VPA_PREFILL_KEYS
-#define VPA_PREFILL_KEYS 32
+#ifndef VPA_PREFILL_STAGES
+#define VPA_PREFILL_STAGES 4
 #endif
-#ifndef VPA_PREFILL_COLS
-#define VPA_PREFILL_COLS 1
-#endif
-constexpr int kPrefillKeys = VPA_PREFILL_KEYS;       // keys per LDS tile (32 or 64)
-constexpr int kPrefillColGroups = VPA_PREFILL_COLS;  // 32-row query groups per wave (1 or 2)
 #ifndef VPA_PREFILL_WAVES_PER_EU
 #define VPA_PREFILL_WAVES_PER_EU 2
 #endif
+constexpr int kPrefillKeys = 32;                    // keys per tile
+constexpr int kPrefillStages = VPA_PREFILL_STAGES;  // LDS tile buffers (tiles in flight + 1)
 constexpr int kPrefillThreads = 256;
+static_assert(kPrefillStages >= 2 && kPrefillStages <= 4, "stages");
+
+// s_waitcnt vmcnt(N), leaving the other counters alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane l's
+// vector lands at lds + 16 * l; the LDS base is wave-uniform.
+__device__ __forceinline__ void dma16(const void* src, const void* lds) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+template <int N>
+using Int = std::integral_constant<int, N>;
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+
+// LDS byte address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// LDS reads of MFMA operands as inline asm. The tiles arrive by DMA, whose
+// completion the kernel waits for explicitly (vmcnt + barrier); reads the
+// compiler sees as ordinary LDS loads would get a conservative wait for
+// every DMA still in flight, later tiles included. The caller waits with
+// lds_wait_* before using the results.
+template <int OFF>
+__device__ __forceinline__ v4i_t lds_read_b128(uint32_t addr) {
+  v4i_t r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ v2i_t lds_read_b64(uint32_t addr) {
+  v2i_t r;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+
+// Value tiles sit in LDS as rows of KT/8 16-byte units (one per 8 keys) whose
+// order is XOR-swizzled by the row, so the MFMA operand reads of 32 rows at
+// once spread over the banks; a DMA lane still writes one contiguous unit.
+template <int U>
+__device__ __forceinline__ int vswz(int d) {
+  return (d >> 1) & (U - 1);
+}
 
 template <typename T, int D, int BS, int G>
 __global__ __launch_bounds__(kPrefillThreads)
@@ -85,30 +151,27 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     int32_t num_heads, int32_t num_kv_heads, int64_t num_blocks, int64_t block_stride,
     int64_t head_stride, int32_t q_tiles) {
   constexpr int KT = kPrefillKeys;
-  constexpr int CG = kPrefillColGroups;
-  constexpr int X = 8;          // 16-bit elements per 16-byte key vector
-  constexpr int ROWS = 32 * CG; // query rows per wave
-  constexpr int PPW = ROWS / G; // query positions per wave
+  constexpr int NS = kPrefillStages;
+  constexpr int X = 8;          // 16-bit elements per 16-byte vector
+  constexpr int PPW = 32 / G;   // query positions per wave
   constexpr int PPB = 4 * PPW;  // query positions per workgroup
-  constexpr int KG = KT / 32;   // 32-key groups of a tile
   constexpr int KS = D / 16;    // k-steps of Q.K^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
-  constexpr int VROW = KT + 4;  // LDS value row (elements): +8 bytes keeps b64 reads conflict-light
-  constexpr int UPT = KT * D / 8 / kPrefillThreads;  // 16-byte units per thread per K / V tile
-  constexpr int KSTEP = kPrefillThreads / KT;        // chunk stride of a thread's K units
-  constexpr int OCT = KT / 8;                        // 8-key octets per value row
-  constexpr int VSTEP = kPrefillThreads / OCT;       // dim stride of a thread's V units
-  static_assert(BS >= 8 && (KT % BS == 0 || BS % KT == 0), "block size");
-  static_assert((KT == 32 || KT == 64) && (CG == 1 || CG == 2) && UPT >= 1, "tile shape");
-  static_assert(ROWS % G == 0 && D % 32 == 0, "rows");
+  constexpr int U = KT / X;     // 16-byte units per value row of a tile
+  constexpr int NU = D * KT / X;                   // 16-byte units per K (and per V) tile
+  constexpr int DPW = NU / kPrefillThreads;        // DMAs per wave per K (and per V) tile
+  constexpr int DPT = 2 * DPW;                     // DMAs per wave per tile
+  constexpr int NBT = KT / BS;                     // blocks per tile
+  static_assert(KT % BS == 0 && BS >= 8 && NU % kPrefillThreads == 0, "tile shape");
 
-  __shared__ __align__(16) uint4 s_k[2][D / X][KT];  // [chunk of 8 dims][key]
-  __shared__ __align__(16) uint16_t s_v[2][D][VROW];  // [dim][key]
-  __shared__ uint64_t s_valid[2];                     // keys of the tile that exist
+  // one LDS object per stage: the compiler then knows that a DMA into one
+  // stage does not alias the operand reads of another
+  // stage buffer: K tile [chunk][key] then V tile [dim][unit ^ swizzle]
+  __shared__ __align__(16) uint4 s_t0[2 * NU], s_t1[2 * NU], s_t2[2 * NU], s_t3[2 * NU];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   // consecutive workgroups: kv heads, then the query tiles of one sequence
   // (heaviest first), so the tiles of a (sequence, kv head) run together on
   // one XCD and share its K/V through L2
@@ -130,221 +193,280 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   const int n_keys = max(0, causal ? min(k_len, wg_end + shift) : k_len);
   const int n_tiles = (n_keys + KT - 1) / KT;
 
-  // this lane's query rows (one per column group; column of S^T and O^T)
+  // this lane's query row (column of S^T and O^T)
   const int col = lane & 31;
   const int half = lane >> 5;
   const int wpos0 = p0 + wave * PPW;
-  bool row_ok[CG];
-  int64_t row[CG];
-  int head[CG], limit[CG];
-#pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    const int ri = cg * 32 + col;
-    const int pos = wpos0 + ri % PPW;
-    head[cg] = j * G + ri / PPW;
-    row_ok[cg] = pos < q_len;
-    row[cg] = (int64_t)qa + pos;
-    limit[cg] = causal ? pos + shift : k_len - 1;  // last key the row sees
-  }
+  const int pos = wpos0 + col % PPW;
+  const int head = j * G + col / PPW;
+  const bool row_ok = pos < q_len;
+  const int64_t row = (int64_t)qa + pos;
+  const int limit = causal ? pos + shift : k_len - 1;  // last key the row sees
   const int wave_end = min(wpos0 + PPW, q_len);
   const int wave_keys =
       wave_end <= wpos0 ? 0 : max(0, causal ? min(k_len, wave_end + shift) : k_len);
   const int wave_min_limit = causal ? wpos0 + shift : k_len - 1;
 
-  uint4 qop[CG][KS];
-#pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    const T* qrow = query + (row[cg] * num_heads + head[cg]) * D + 8 * half;
+  uint4 qop[KS];
+  {
+    const T* qrow = query + (row * num_heads + head) * D + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      qop[cg][ks] =
-          row_ok[cg] ? *reinterpret_cast<const uint4*>(qrow + 16 * ks) : make_uint4(0, 0, 0, 0);
+      qop[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks) : make_uint4(0, 0, 0, 0);
   }
 
-  f32x16_t o[CG][DT];
-  float m[CG], lsum[CG];  // running max (log2 units) and this lane's share of the sum
+  f32x16_t o[DT];
 #pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    m[cg] = -INFINITY;
-    lsum[cg] = 0.f;
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[cg][dt][e] = 0.f;
-  }
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+  float m = -INFINITY;  // running max of the row, log2 units
+  float lsum = 0.f;     // this lane's share of the row's exp sum
 
   const T* kbase = key_cache + (int64_t)j * head_stride;
   const T* vbase = value_cache + (int64_t)j * head_stride;
   const uint32_t* bt = block_tables + (int64_t)s * block_table_stride;
-  // loader roles: K units hold key tid % KT of chunks tid / KT + KSTEP i;
-  // V units hold keys 8 (tid % OCT) .. +7 of dims tid / OCT + VSTEP i
-  const int lk = tid % KT;
-  const int lc = tid / KT;
-  const int lo = tid % OCT;
-  const int ld = tid / OCT;
-  uint4 kreg[UPT], vreg[UPT];
-  bool kvalid = false;
+  const int last_blk = max(k_len - 1, 0) / BS;
 
-  auto load_tile = [&](int tt) {
-    const int k0 = tt * KT;
-    {
-      const int key = k0 + lk;
-      uint32_t phys = key < k_len ? bt[key / BS] : 0u;
-      kvalid = key < k_len && (int64_t)phys < num_blocks;
-      if (!kvalid) phys = 0u;  // read block 0 (in bounds); the key is masked
-      const T* src = kbase + (int64_t)phys * block_stride + (key % BS) * X;
+  auto kst = [&](auto sc) -> uint4* {
+    constexpr int S = decltype(sc)::value;
+    if constexpr (S == 0) return s_t0;
+    else if constexpr (S == 1) return s_t1;
+    else if constexpr (S == 2) return s_t2;
+    else return s_t3;
+  };
+  auto vst = [&](auto sc) -> uint4* { return kst(sc) + NU; };
+  // block ids of a tile (uniform: scalar loads; the index is clamped to the
+  // sequence's last block, which exists whenever a tile is touched)
+  auto tile_blocks = [&](int k0, uint32_t (&pb)[NBT]) {
 #pragma unroll
-      for (int i = 0; i < UPT; ++i)
-        kreg[i] = *reinterpret_cast<const uint4*>(src + (int64_t)(lc + KSTEP * i) * BS * X);
+    for (int i = 0; i < NBT; ++i)
+      pb[i] = bt[__builtin_amdgcn_readfirstlane(min(k0 / BS + i, last_blk))];
+  };
+  auto block_of = [&](const uint32_t (&pb)[NBT], int i) {
+    uint32_t v = pb[0];
+#pragma unroll
+    for (int k = 1; k < NBT; ++k)
+      if (i == k) v = pb[k];
+    return v;
+  };
+
+  // Issue the DMAs of tile t into stage S. Keys past the context or in
+  // absent blocks read block 0 (in bounds); they are masked in S and their
+  // values zeroed when the V operands are built.
+  auto issue = [&](auto sc, int t) {
+    const int k0 = t * KT;
+    uint32_t pb[NBT];
+    tile_blocks(k0, pb);
+    uint4* sk = kst(sc);
+    uint4* sv = vst(sc);
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+      const int q = (wave * DPW + i) * 64 + lane;  // K unit q: chunk q / KT, key q % KT
+      const int key = q % KT;
+      uint32_t phys = block_of(pb, key / BS);
+      phys = (k0 + key < k_len && (int64_t)phys < num_blocks) ? phys : 0u;
+      dma16(kbase + (int64_t)phys * block_stride + ((q / KT) * BS + key % BS) * X,
+            sk + (wave * DPW + i) * 64);
     }
-    {
-      const int key = k0 + 8 * lo;
-      uint32_t phys = key < k_len ? bt[key / BS] : 0u;
-      const bool ok = key < k_len && (int64_t)phys < num_blocks;
-      if (!ok) phys = 0u;
-      const T* src = vbase + (int64_t)phys * block_stride + (key % BS);
 #pragma unroll
-      for (int i = 0; i < UPT; ++i)
-        vreg[i] = *reinterpret_cast<const uint4*>(src + (int64_t)(ld + VSTEP * i) * BS);
-      // values of keys that do not exist are zeroed (stale cache contents
-      // could be NaN, and 0 * NaN would poison the sum)
-      const int nvalid = ok ? min(8, k_len - key) : 0;
-      if (nvalid < 8) {
-#pragma unroll
-        for (int i = 0; i < UPT; ++i) {
-          uint32_t w[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (e >= nvalid) w[e / 2] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
-          vreg[i] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-      }
+    for (int i = 0; i < DPW; ++i) {
+      const int q = (wave * DPW + i) * 64 + lane;  // V unit q: row q / U, keys 8u .. 8u+7
+      const int d = q / U;
+      const int u = (q % U) ^ vswz<U>(d);
+      uint32_t phys = block_of(pb, (8 * u) / BS);
+      phys = (k0 + 8 * u < k_len && (int64_t)phys < num_blocks) ? phys : 0u;
+      dma16(vbase + (int64_t)phys * block_stride + (int64_t)d * BS + (8 * u) % BS,
+            sv + (wave * DPW + i) * 64);
     }
   };
-  auto store_tile = [&](int b) {
-#pragma unroll
-    for (int i = 0; i < UPT; ++i) s_k[b][lc + KSTEP * i][lk] = kreg[i];
-#pragma unroll
-    for (int i = 0; i < UPT; ++i) {
-      uint2* dst = reinterpret_cast<uint2*>(&s_v[b][ld + VSTEP * i][8 * lo]);
-      dst[0] = make_uint2(vreg[i].x, vreg[i].y);
-      dst[1] = make_uint2(vreg[i].z, vreg[i].w);
-    }
-    // lanes 0..KT-1 of wave 0 hold keys 0..KT-1 of the tile
-    if (wave == 0) {
-      const uint64_t bal = __ballot(kvalid);
-      if (lane == 0) s_valid[b] = KT == 64 ? bal : (bal & 0xffffffffull);
-    }
-  };
-  auto compute_tile = [&](int tt, int b) {
-    const int k0 = tt * KT;
+
+  auto compute = [&](auto sc, int t) {
+    const int k0 = t * KT;
     if (k0 >= wave_keys) return;  // no row of this wave sees these keys
-    const uint64_t vmask = s_valid[b];
-    const bool full =
-        vmask == (KT == 64 ? ~0ull : 0xffffffffull) && k0 + KT - 1 <= wave_min_limit;
-    // S^T = K . Q^T: every K operand read from LDS feeds CG MFMAs
-    f32x16_t sacc[KG][CG];
+    const uint4* sk = kst(sc);
+    const uint4* sv = vst(sc);
+    uint32_t pb[NBT];
+    tile_blocks(k0, pb);
+    // keys of the tile that exist: inside the context and in a present block
+    uint32_t vmask = 0;
 #pragma unroll
-    for (int kg = 0; kg < KG; ++kg)
+    for (int kb = 0; kb < NBT; ++kb)
+      if ((int64_t)pb[kb] < num_blocks)
+        vmask |= (BS >= 32 ? 0xffffffffu : ((1u << BS) - 1u)) << (kb * BS);
+    const int nk = k_len - k0;
+    if (nk < KT) vmask &= (1u << max(nk, 0)) - 1u;
+    const bool full = vmask == 0xffffffffu && k0 + KT - 1 <= wave_min_limit;
+
+    // S^T = K . Q^T; the K operand of k-step ks is chunk 2 ks + half, key col
+    const uint32_t ka = lds_addr(sk + half * KT + col);
+    v4i_t kop[KS];
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      ((kop[I] = lds_read_b128<I * 2 * KT * 16>(ka)), ...);
+    }(std::make_integer_sequence<int, KS>{});
+    if constexpr (KS == 8) {
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kop[0]), "+v"(kop[1]), "+v"(kop[2]),
+                   "+v"(kop[3]), "+v"(kop[4]), "+v"(kop[5]), "+v"(kop[6]), "+v"(kop[7]));
+    } else {
+      static_assert(KS == 4, "head_dim 64 or 128");
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kop[0]), "+v"(kop[1]), "+v"(kop[2]),
+                   "+v"(kop[3]));
+    }
+    f32x16_t sacc;
 #pragma unroll
-      for (int cg = 0; cg < CG; ++cg)
+    for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[kg][cg][e] = 0.f;
+    for (int ks = 0; ks < KS; ++ks)
+      sacc = mfma32x32x16<T>(__builtin_bit_cast(uint4, kop[ks]), qop[ks], sacc);
+
+    // online softmax of the row; P^T operands straight from the accumulator
+    float sval[16];
+    float mx = -INFINITY;
+    if (full) {
 #pragma unroll
-    for (int kg = 0; kg < KG; ++kg)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint4 a = s_k[b][2 * ks + half][32 * kg + col];
-#pragma unroll
-        for (int cg = 0; cg < CG; ++cg)
-          sacc[kg][cg] = mfma32x32x16<T>(a, qop[cg][ks], sacc[kg][cg]);
+      for (int r = 0; r < 16; ++r) {
+        sval[r] = sacc[r] * scale_log2;
+        mx = fmaxf(mx, sval[r]);
       }
-    // online softmax per row; P^T operands straight from the accumulators
-    uint4 pk[CG][2 * KG];
+    } else {
 #pragma unroll
-    for (int cg = 0; cg < CG; ++cg) {
-      float sv[KG][16];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kg = 0; kg < KG; ++kg)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = 32 * kg + 8 * (r / 4) + 4 * half + (r % 4);  // row of element r
-          float v = sacc[kg][cg][r] * scale_log2;
-          if (!full) v = (((vmask >> key) & 1ull) && k0 + key <= limit[cg]) ? v : -INFINITY;
-          sv[kg][r] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = max_xor32(mx);
-      const float m_new = fmaxf(m[cg], mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m[cg] - m_use);
-      float ps = 0.f;
-#pragma unroll
-      for (int kg = 0; kg < KG; ++kg)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sv[kg][r] = exp2f(sv[kg][r] - m_use);
-          ps += sv[kg][r];
-        }
-      lsum[cg] = lsum[cg] * alpha + ps;
-      m[cg] = m_new;
+      for (int r = 0; r < 16; ++r) {
+        const int key = 8 * (r / 4) + 4 * half + (r % 4);  // accumulator row of element r
+        const bool ok = ((vmask >> key) & 1u) && k0 + key <= limit;
+        sval[r] = ok ? sacc[r] * scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sval[r]);
+      }
+    }
+    mx = max_xor32(mx);
+    // The reference max m only moves when some row's tile max exceeds it by
+    // more than kRescaleSlack (log2 units): the probabilities stay below
+    // 2^kRescaleSlack, and O and the row sums are rescaled only then.
+    constexpr float kRescaleSlack = 8.f;
+    if (__ballot(mx > m + kRescaleSlack) != 0) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
+      lsum *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o[cg][dt][e] *= alpha;
-#pragma unroll
-      for (int k2 = 0; k2 < 2 * KG; ++k2) {
-        const float* p = &sv[k2 / 2][8 * (k2 % 2)];
-        pk[cg][k2] = make_uint4(pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]),
-                                pack2<T>(p[4], p[5]), pack2<T>(p[6], p[7]));
-      }
+        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+      m = m_new;
     }
-    // O^T += V^T . P^T: k-step k2 covers keys 16 k2 + {4h..4h+3, 8+4h..8+4h+3}
+    const float m_use = m == -INFINITY ? 0.f : m;  // a row without keys so far
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sval[r] = __builtin_amdgcn_exp2f(sval[r] - m_use);
+      ps += sval[r];
+    }
+    lsum += ps;
+    uint4 pk[2];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+      pk[k2] = make_uint4(pack2_hw<T>(sval[8 * k2 + 0], sval[8 * k2 + 1]),
+                          pack2_hw<T>(sval[8 * k2 + 2], sval[8 * k2 + 3]),
+                          pack2_hw<T>(sval[8 * k2 + 4], sval[8 * k2 + 5]),
+                          pack2_hw<T>(sval[8 * k2 + 6], sval[8 * k2 + 7]));
+    // per-key 16-bit masks of the V operands: values of keys that do not
+    // exist are zeroed (stale slots may hold NaN, and 0 * NaN poisons O)
+    auto keymask2 = [&](int key) {
+      const uint32_t b = (vmask >> key) & 3u;
+      return ((b & 1u) ? 0x0000ffffu : 0u) | ((b & 2u) ? 0xffff0000u : 0u);
+    };
+
+    // O^T += V^T . P^T: k-step k2 covers keys 16 k2 + {4h..4h+3, 8+4h..8+4h+3},
+    // i.e. the half `half` of units 2 k2 and 2 k2 + 1 of row d = 32 dt + col
+    // (rows 32 apart are 32 * U * 16 bytes apart and share the swizzle)
+    const int sw = vswz<U>(col);
+    const uint32_t va = lds_addr(sv + col * U) + 8 * half;
+    const uint32_t va0 = va + 16 * (0 ^ sw), va1 = va + 16 * (1 ^ sw);
+    const uint32_t va2 = va + 16 * (2 ^ sw), va3 = va + 16 * (3 ^ sw);
+    constexpr int RS = 32 * U * 16;  // bytes between rows d and d + 32
+    v2i_t vop[DT][4];
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      ((vop[I][0] = lds_read_b64<I * RS>(va0), vop[I][1] = lds_read_b64<I * RS>(va1),
+        vop[I][2] = lds_read_b64<I * RS>(va2), vop[I][3] = lds_read_b64<I * RS>(va3)), ...);
+    }(std::make_integer_sequence<int, DT>{});
+    if constexpr (DT == 4) {
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[0][2]), "+v"(vop[0][3]),
+                     "+v"(vop[1][0]), "+v"(vop[1][1]), "+v"(vop[1][2]), "+v"(vop[1][3]),
+                     "+v"(vop[2][0]), "+v"(vop[2][1]), "+v"(vop[2][2]), "+v"(vop[2][3]),
+                     "+v"(vop[3][0]), "+v"(vop[3][1]), "+v"(vop[3][2]), "+v"(vop[3][3]));
+    } else {
+      static_assert(DT == 2, "head_dim 64 or 128");
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[0][2]), "+v"(vop[0][3]),
+                     "+v"(vop[1][0]), "+v"(vop[1][1]), "+v"(vop[1][2]), "+v"(vop[1][3]));
+    }
+    if (vmask != 0xffffffffu) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const int kl = 16 * k2 + 4 * half;
+          vop[dt][2 * k2][0] &= keymask2(kl);
+          vop[dt][2 * k2][1] &= keymask2(kl + 2);
+          vop[dt][2 * k2 + 1][0] &= keymask2(kl + 8);
+          vop[dt][2 * k2 + 1][1] &= keymask2(kl + 10);
+        }
+    }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-      for (int k2 = 0; k2 < 2 * KG; ++k2) {
-        const uint16_t* vr = &s_v[b][32 * dt + col][16 * k2 + 4 * half];
-        const uint2 lo4 = *reinterpret_cast<const uint2*>(vr);
-        const uint2 hi4 = *reinterpret_cast<const uint2*>(vr + 8);
-        const uint4 a = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
-#pragma unroll
-        for (int cg = 0; cg < CG; ++cg) o[cg][dt] = mfma32x32x16<T>(a, pk[cg][k2], o[cg][dt]);
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const v2i_t lo4 = vop[dt][2 * k2];
+        const v2i_t hi4 = vop[dt][2 * k2 + 1];
+        o[dt] = mfma32x32x16<T>(make_uint4(lo4[0], lo4[1], hi4[0], hi4[1]), pk[k2], o[dt]);
       }
     }
   };
 
+  // one pipeline step: wait for tile t, refill the stage tile t-1 used with
+  // tile t + NS - 1, compute tile t
+  auto step = [&](auto sc, int t) {
+    if (t >= n_tiles) return;
+    constexpr int S = decltype(sc)::value;
+    const int after = min(NS - 2, n_tiles - 1 - t);  // later tiles already issued
+    if (after >= 2) wait_vmcnt<2 * DPT>();
+    else if (after == 1) wait_vmcnt<DPT>();
+    else wait_vmcnt<0>();
+    // tile t is in LDS for every wave, and every wave is done with tile t-1.
+    // A bare s_barrier: __syncthreads() would also fence this wave's LDS
+    // writes, i.e. wait for all of its outstanding DMAs, later tiles
+    // included; the explicit vmcnt wait above already covers tile t.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (t + NS - 1 < n_tiles) issue(Int<(S + NS - 1) % NS>{}, t + NS - 1);
+    compute(sc, t);
+  };
+
   if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int tt = 0; tt < n_tiles; ++tt) {
-      const int b = tt & 1;
-      const bool more = tt + 1 < n_tiles;
-      if (more) load_tile(tt + 1);  // in flight during this tile's MFMAs
-      compute_tile(tt, b);
-      if (more) store_tile(b ^ 1);
-      __syncthreads();
+    issue(Int<0>{}, 0);
+    if (NS > 2 && 1 < n_tiles) issue(Int<1 % NS>{}, 1);
+    if (NS > 3 && 2 < n_tiles) issue(Int<2 % NS>{}, 2);
+    for (int t0 = 0; t0 < n_tiles; t0 += NS) {
+      step(Int<0>{}, t0);
+      step(Int<1 % NS>{}, t0 + 1);
+      if constexpr (NS > 2) step(Int<2 % NS>{}, t0 + 2);
+      if constexpr (NS > 3) step(Int<3 % NS>{}, t0 + 3);
     }
   }
 
+  const float total = sum_xor32(lsum);
+  const float inv = total > 0.f ? 1.f / total : 0.f;  // a row that sees no key gives 0
+  if (row_ok) {
+    T* orow = out + (row * num_heads + head) * D;
 #pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    const float total = sum_xor32(lsum[cg]);
-    const float inv = total > 0.f ? 1.f / total : 0.f;  // a row that sees no key gives 0
-    if (row_ok[cg]) {
-      T* orow = out + (row[cg] * num_heads + head[cg]) * D;
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d0 = 32 * dt + 8 * i + 4 * half;
-          *reinterpret_cast<uint2*>(orow + d0) =
-              make_uint2(pack2<T>(o[cg][dt][4 * i] * inv, o[cg][dt][4 * i + 1] * inv),
-                         pack2<T>(o[cg][dt][4 * i + 2] * inv, o[cg][dt][4 * i + 3] * inv));
-        }
-    }
+      for (int i = 0; i < 4; ++i) {
+        const int d0 = 32 * dt + 8 * i + 4 * half;
+        *reinterpret_cast<uint2*>(orow + d0) =
+            make_uint2(pack2_hw<T>(o[dt][4 * i] * inv, o[dt][4 * i + 1] * inv),
+                       pack2_hw<T>(o[dt][4 * i + 2] * inv, o[dt][4 * i + 3] * inv));
+      }
   }
 }
 
@@ -356,7 +478,7 @@ hipError_t launch_prefill_t(void* out, const void* query, const void* key_cache,
                             int32_t max_query_len, int32_t max_kv_len, int64_t total_query_rows,
                             float scale, int32_t causal, int32_t num_heads, const CacheGeom& g,
                             hipStream_t stream) {
-  constexpr int kPositions = 4 * 32 * kPrefillColGroups / G;
+  constexpr int kPositions = 4 * 32 / G;
   const int q_tiles = (max_query_len + kPositions - 1) / kPositions;
   const int64_t grid = (int64_t)num_seqs * q_tiles * g.num_kv_heads;
   if (grid == 0) return hipSuccess;
@@ -450,7 +572,7 @@ bool prefill_supported(int dtype, int head_dim, int block_size, int group) {
          (group == 1 || group == 2 || group == 4);
 }
 
-int prefill_positions_per_workgroup(int group) { return 4 * 32 * kPrefillColGroups / group; }
+int prefill_positions_per_workgroup(int group) { return 4 * 32 / group; }
 
 hipError_t launch_prefill_paged(int dtype, void* out, const void* query, const void* key_cache,
                                 const void* value_cache, const uint32_t* block_tables,

@@ -90,6 +90,23 @@ __device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) {
   return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
 }
 
+// The same packing with gfx950's v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32
+// (round to nearest even, one instruction, no branches; a NaN comes out as
+// the canonical quiet NaN).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v_t __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ uint32_t pack2_hw(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2_hw<bf16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2v_t));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2_hw<f16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2v_t));
+}
+
 // acc + a.lo*b.lo + a.hi*b.hi for two packed 16-bit pairs (v_dot2 on gfx950).
 template <typename T>
 __device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float acc);
