@@ -34,8 +34,13 @@
 // explicit vmcnt counts plus a bare workgroup barrier (the compiler's
 // __syncthreads would drain every outstanding DMA), and the operand reads
 // from LDS are written as ds_read with their own lgkmcnt wait so the
-// compiler does not add a full vmcnt drain before them. V is stored [dim]
-// [key] with its 16-byte units XOR-swizzled by dim to spread the banks.
+// compiler does not add a full vmcnt drain before them. Each DMA copies 64
+// units of one cache block, so its address is a scalar block base plus a
+// fixed per-lane offset. In LDS, K keeps the block's [chunk][key] order and
+// V is transposed to [8-key unit][dim]; with the tile's keys permuted inside
+// every 16 (tile_key_of_row), each MFMA operand is one 16-byte LDS read and
+// every 16-lane read pass covers 256 contiguous bytes (no bank conflicts on
+// gfx950's 64 four-byte banks).
 //
 // Softmax: scores are in log2 units (scale * log2 e folded into the scale);
 // the running max only moves when a tile's max exceeds it by more than
@@ -107,7 +112,6 @@ template <int N>
 using Int = std::integral_constant<int, N>;
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
-typedef int v2i_t __attribute__((ext_vector_type(2)));
 
 // LDS byte address of a __shared__ pointer.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -117,27 +121,21 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // LDS reads of MFMA operands as inline asm. The tiles arrive by DMA, whose
 // completion the kernel waits for explicitly (vmcnt + barrier); reads the
 // compiler sees as ordinary LDS loads would get a conservative wait for
-// every DMA still in flight, later tiles included. The caller waits with
-// lds_wait_* before using the results.
+// every DMA still in flight, later tiles included. The caller issues an
+// s_waitcnt lgkmcnt(0) that names the results before using them.
 template <int OFF>
 __device__ __forceinline__ v4i_t lds_read_b128(uint32_t addr) {
   v4i_t r;
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
   return r;
 }
-template <int OFF>
-__device__ __forceinline__ v2i_t lds_read_b64(uint32_t addr) {
-  v2i_t r;
-  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-  return r;
-}
 
-// Value tiles sit in LDS as rows of KT/8 16-byte units (one per 8 keys) whose
-// order is XOR-swizzled by the row, so the MFMA operand reads of 32 rows at
-// once spread over the banks; a DMA lane still writes one contiguous unit.
-template <int U>
-__device__ __forceinline__ int vswz(int d) {
-  return (d >> 1) & (U - 1);
+// Key held in row i of the S^T tile: bits 2 and 3 of i swapped. Lane half h
+// of the 32x32 accumulator holds rows {4h..4h+3, 8+4h..8+4h+3} of every 16;
+// through this order those rows are keys 8h..8h+7, one whole 16-byte unit of
+// a value row, so the P^T operand of a k-step pairs with one aligned V read.
+__device__ __forceinline__ constexpr int tile_key_of_row(int i) {
+  return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
 }
 
 template <typename T, int D, int BS, int G>
@@ -157,17 +155,25 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   constexpr int PPB = 4 * PPW;  // query positions per workgroup
   constexpr int KS = D / 16;    // k-steps of Q.K^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
-  constexpr int U = KT / X;     // 16-byte units per value row of a tile
+  constexpr int UB = BS / X;    // 16-byte units per value row of a block
   constexpr int NU = D * KT / X;                   // 16-byte units per K (and per V) tile
   constexpr int DPW = NU / kPrefillThreads;        // DMAs per wave per K (and per V) tile
   constexpr int DPT = 2 * DPW;                     // DMAs per wave per tile
   constexpr int NBT = KT / BS;                     // blocks per tile
-  static_assert(KT % BS == 0 && BS >= 8 && NU % kPrefillThreads == 0, "tile shape");
+  constexpr int RBV = D * UB;                      // units of one block's K (or V) rows
+  constexpr int DPB = RBV / 64;                    // DMAs per block region
+  // LDS units between the K regions of two blocks: with 8-key blocks, the 16
+  // lanes of one LDS read pass span two blocks, padded to other banks
+  constexpr int RBK = RBV + (BS == 8 ? 8 : 0);
+  constexpr int KU = NBT * RBK;                    // K units of a stage
+  static_assert(KT % BS == 0 && BS >= 8 && NU % kPrefillThreads == 0 && RBV % 64 == 0 &&
+                    (kPrefillThreads / 64 * DPW) % DPB == 0,
+                "tile shape");
 
   // one LDS object per stage: the compiler then knows that a DMA into one
-  // stage does not alias the operand reads of another
-  // stage buffer: K tile [chunk][key] then V tile [dim][unit ^ swizzle]
-  __shared__ __align__(16) uint4 s_t0[2 * NU], s_t1[2 * NU], s_t2[2 * NU], s_t3[2 * NU];
+  // stage does not alias the operand reads of another.
+  // stage buffer: K regions [block][chunk][key], then V regions [block][unit][dim]
+  __shared__ __align__(16) uint4 s_t0[KU + NU], s_t1[KU + NU], s_t2[KU + NU], s_t3[KU + NU];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -213,6 +219,17 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qop[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks) : make_uint4(0, 0, 0, 0);
+    // a negative scale is folded into Q (a sign flip, exact in the cache
+    // type), so the row max can be taken on the raw scores
+    if (scale_log2 < 0.f) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        qop[ks].x ^= 0x80008000u;
+        qop[ks].y ^= 0x80008000u;
+        qop[ks].z ^= 0x80008000u;
+        qop[ks].w ^= 0x80008000u;
+      }
+    }
   }
 
   f32x16_t o[DT];
@@ -220,6 +237,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+  const float sl = fabsf(scale_log2);
   float m = -INFINITY;  // running max of the row, log2 units
   float lsum = 0.f;     // this lane's share of the row's exp sum
 
@@ -235,7 +253,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     else if constexpr (S == 2) return s_t2;
     else return s_t3;
   };
-  auto vst = [&](auto sc) -> uint4* { return kst(sc) + NU; };
+  auto vst = [&](auto sc) -> uint4* { return kst(sc) + KU; };
   // block ids of a tile (uniform: scalar loads; the index is clamped to the
   // sequence's last block, which exists whenever a tile is touched)
   auto tile_blocks = [&](int k0, uint32_t (&pb)[NBT]) {
@@ -243,17 +261,21 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     for (int i = 0; i < NBT; ++i)
       pb[i] = bt[__builtin_amdgcn_readfirstlane(min(k0 / BS + i, last_blk))];
   };
-  auto block_of = [&](const uint32_t (&pb)[NBT], int i) {
-    uint32_t v = pb[0];
+  // Every DMA copies 64 units of one block (DPB DMAs per block region), so
+  // its global base is uniform and each lane adds a fixed element offset:
+  // K regions are plain copies of the block's [chunk][key] units, V regions
+  // transpose the block's [dim][unit] rows to [unit][dim].
+  uint32_t koff[DPW], voff[DPW];
 #pragma unroll
-    for (int k = 1; k < NBT; ++k)
-      if (i == k) v = pb[k];
-    return v;
-  };
+  for (int i = 0; i < DPW; ++i) {
+    const int r = ((wave * DPW + i) % DPB) * 64 + lane;  // unit of the block region
+    koff[i] = (uint32_t)(r * X);
+    voff[i] = (uint32_t)((r % D) * BS + (r / D) * X);
+  }
 
-  // Issue the DMAs of tile t into stage S. Keys past the context or in
-  // absent blocks read block 0 (in bounds); they are masked in S and their
-  // values zeroed when the V operands are built.
+  // Issue the DMAs of tile t into stage S. Keys past the context and absent
+  // blocks read block 0 (in bounds); they are masked in S and their values
+  // zeroed when the V operands are built.
   auto issue = [&](auto sc, int t) {
     const int k0 = t * KT;
     uint32_t pb[NBT];
@@ -262,24 +284,30 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     uint4* sv = vst(sc);
 #pragma unroll
     for (int i = 0; i < DPW; ++i) {
-      const int q = (wave * DPW + i) * 64 + lane;  // K unit q: chunk q / KT, key q % KT
-      const int key = q % KT;
-      uint32_t phys = block_of(pb, key / BS);
-      phys = (k0 + key < k_len && (int64_t)phys < num_blocks) ? phys : 0u;
-      dma16(kbase + (int64_t)phys * block_stride + ((q / KT) * BS + key % BS) * X,
-            sk + (wave * DPW + i) * 64);
-    }
+      const int di = wave * DPW + i;  // uniform
+      const int b = di / DPB;
+      uint32_t phys = pb[0];
 #pragma unroll
-    for (int i = 0; i < DPW; ++i) {
-      const int q = (wave * DPW + i) * 64 + lane;  // V unit q: row q / U, keys 8u .. 8u+7
-      const int d = q / U;
-      const int u = (q % U) ^ vswz<U>(d);
-      uint32_t phys = block_of(pb, (8 * u) / BS);
-      phys = (k0 + 8 * u < k_len && (int64_t)phys < num_blocks) ? phys : 0u;
-      dma16(vbase + (int64_t)phys * block_stride + (int64_t)d * BS + (8 * u) % BS,
-            sv + (wave * DPW + i) * 64);
+      for (int k = 1; k < NBT; ++k)
+        if (b == k) phys = pb[k];
+      phys = (k0 + b * BS < k_len && (int64_t)phys < num_blocks) ? phys : 0u;
+      phys = __builtin_amdgcn_readfirstlane(phys);
+      const int64_t blk = (int64_t)phys * block_stride;
+      dma16(kbase + blk + koff[i], sk + b * RBK + (di % DPB) * 64);
+      dma16(vbase + blk + voff[i], sv + b * RBV + (di % DPB) * 64);
     }
   };
+
+  // LDS byte offsets of this lane's operand reads within a stage
+  const uint32_t ka_lane = [&] {
+    const int key = tile_key_of_row(col);
+    return (uint32_t)(((key / BS) * RBK + half * BS + key % BS) * 16);
+  }();
+  // unit group g = 2 k2 + half of the tile (keys 8g .. 8g+7) sits at
+  // (g / UB) * RBV + (g % UB) * D units; that splits into a k2 and a half term
+  auto vgroup = [](int g) { return (g / UB) * RBV + (g % UB) * D; };
+  constexpr int kVStep1 = ((2 / UB) * RBV + (2 % UB) * D) * 16;
+  const uint32_t va_lane = (uint32_t)((vgroup(half) + col) * 16);
 
   auto compute = [&](auto sc, int t) {
     const int k0 = t * KT;
@@ -298,11 +326,11 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     if (nk < KT) vmask &= (1u << max(nk, 0)) - 1u;
     const bool full = vmask == 0xffffffffu && k0 + KT - 1 <= wave_min_limit;
 
-    // S^T = K . Q^T; the K operand of k-step ks is chunk 2 ks + half, key col
-    const uint32_t ka = lds_addr(sk + half * KT + col);
+    // S^T = K . Q^T; the K operand of k-step ks is chunk 2 ks + half of the
+    // key in row col
     v4i_t kop[KS];
     [&]<int... I>(std::integer_sequence<int, I...>) {
-      ((kop[I] = lds_read_b128<I * 2 * KT * 16>(ka)), ...);
+      ((kop[I] = lds_read_b128<I * 2 * BS * 16>(ka_lane + lds_addr(sk))), ...);
     }(std::make_integer_sequence<int, KS>{});
     if constexpr (KS == 8) {
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kop[0]), "+v"(kop[1]), "+v"(kop[2]),
@@ -319,25 +347,26 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     for (int ks = 0; ks < KS; ++ks)
       sacc = mfma32x32x16<T>(__builtin_bit_cast(uint4, kop[ks]), qop[ks], sacc);
 
-    // online softmax of the row; P^T operands straight from the accumulator
+    // online softmax of the row on the raw scores (the scale is positive);
+    // P^T operands straight from the accumulator
     float sval[16];
     float mx = -INFINITY;
     if (full) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        sval[r] = sacc[r] * scale_log2;
+        sval[r] = sacc[r];
         mx = fmaxf(mx, sval[r]);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = 8 * (r / 4) + 4 * half + (r % 4);  // accumulator row of element r
+        const int key = 16 * (r / 8) + 8 * half + r % 8;  // key of element r
         const bool ok = ((vmask >> key) & 1u) && k0 + key <= limit;
-        sval[r] = ok ? sacc[r] * scale_log2 : -INFINITY;
+        sval[r] = ok ? sacc[r] : -INFINITY;
         mx = fmaxf(mx, sval[r]);
       }
     }
-    mx = max_xor32(mx);
+    mx = max_xor32(mx) * sl;
     // The reference max m only moves when some row's tile max exceeds it by
     // more than kRescaleSlack (log2 units): the probabilities stay below
     // 2^kRescaleSlack, and O and the row sums are rescaled only then.
@@ -356,7 +385,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      sval[r] = __builtin_amdgcn_exp2f(sval[r] - m_use);
+      sval[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sval[r], sl, -m_use));
       ps += sval[r];
     }
     lsum += ps;
@@ -374,52 +403,42 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
       return ((b & 1u) ? 0x0000ffffu : 0u) | ((b & 2u) ? 0xffff0000u : 0u);
     };
 
-    // O^T += V^T . P^T: k-step k2 covers keys 16 k2 + {4h..4h+3, 8+4h..8+4h+3},
-    // i.e. the half `half` of units 2 k2 and 2 k2 + 1 of row d = 32 dt + col
-    // (rows 32 apart are 32 * U * 16 bytes apart and share the swizzle)
-    const int sw = vswz<U>(col);
-    const uint32_t va = lds_addr(sv + col * U) + 8 * half;
-    const uint32_t va0 = va + 16 * (0 ^ sw), va1 = va + 16 * (1 ^ sw);
-    const uint32_t va2 = va + 16 * (2 ^ sw), va3 = va + 16 * (3 ^ sw);
-    constexpr int RS = 32 * U * 16;  // bytes between rows d and d + 32
-    v2i_t vop[DT][4];
+    // O^T += V^T . P^T: k-step k2 of lane half h covers keys 16 k2 + 8h ..
+    // 16 k2 + 8h + 7, one unit of row d = 32 dt + col
+    v4i_t vop[DT][2];
     [&]<int... I>(std::integer_sequence<int, I...>) {
-      ((vop[I][0] = lds_read_b64<I * RS>(va0), vop[I][1] = lds_read_b64<I * RS>(va1),
-        vop[I][2] = lds_read_b64<I * RS>(va2), vop[I][3] = lds_read_b64<I * RS>(va3)), ...);
+      ((vop[I][0] = lds_read_b128<I * 32 * 16>(va_lane + lds_addr(sv)),
+        vop[I][1] = lds_read_b128<I * 32 * 16 + kVStep1>(va_lane + lds_addr(sv))), ...);
     }(std::make_integer_sequence<int, DT>{});
     if constexpr (DT == 4) {
       asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[0][2]), "+v"(vop[0][3]),
-                     "+v"(vop[1][0]), "+v"(vop[1][1]), "+v"(vop[1][2]), "+v"(vop[1][3]),
-                     "+v"(vop[2][0]), "+v"(vop[2][1]), "+v"(vop[2][2]), "+v"(vop[2][3]),
-                     "+v"(vop[3][0]), "+v"(vop[3][1]), "+v"(vop[3][2]), "+v"(vop[3][3]));
+                   : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[1][0]), "+v"(vop[1][1]),
+                     "+v"(vop[2][0]), "+v"(vop[2][1]), "+v"(vop[3][0]), "+v"(vop[3][1]));
     } else {
       static_assert(DT == 2, "head_dim 64 or 128");
       asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[0][2]), "+v"(vop[0][3]),
-                     "+v"(vop[1][0]), "+v"(vop[1][1]), "+v"(vop[1][2]), "+v"(vop[1][3]));
+                   : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[1][0]), "+v"(vop[1][1]));
     }
     if (vmask != 0xffffffffu) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) {
-          const int kl = 16 * k2 + 4 * half;
-          vop[dt][2 * k2][0] &= keymask2(kl);
-          vop[dt][2 * k2][1] &= keymask2(kl + 2);
-          vop[dt][2 * k2 + 1][0] &= keymask2(kl + 8);
-          vop[dt][2 * k2 + 1][1] &= keymask2(kl + 10);
-        }
-    }
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
-        const v2i_t lo4 = vop[dt][2 * k2];
-        const v2i_t hi4 = vop[dt][2 * k2 + 1];
-        o[dt] = mfma32x32x16<T>(make_uint4(lo4[0], lo4[1], hi4[0], hi4[1]), pk[k2], o[dt]);
+        const int kl = 16 * k2 + 8 * half;
+        const uint32_t m0 = keymask2(kl), m1 = keymask2(kl + 2), m2 = keymask2(kl + 4),
+                       m3 = keymask2(kl + 6);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          vop[dt][k2][0] &= m0;
+          vop[dt][k2][1] &= m1;
+          vop[dt][k2][2] &= m2;
+          vop[dt][k2][3] &= m3;
+        }
       }
     }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+        o[dt] = mfma32x32x16<T>(__builtin_bit_cast(uint4, vop[dt][k2]), pk[k2], o[dt]);
   };
 
   // one pipeline step: wait for tile t, refill the stage tile t-1 used with

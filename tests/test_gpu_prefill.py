@@ -23,7 +23,7 @@ NAN16 = {orc.BF16: 0x7FC0, orc.F16: 0x7E00}
 
 def prefill_case(device, code, h, kvh, d, bs, prior, qlens, seed, causal=True, nb=None,
                  mutate_bt=None, stale_nan=False, max_query_len=None, max_context_len=None,
-                 pad_cols=0):
+                 pad_cols=0, scale=None):
     rng = np.random.default_rng(seed)
     prior = np.asarray(prior, dtype=np.int64)
     qlens = np.asarray(qlens, dtype=np.int64)
@@ -48,7 +48,7 @@ def prefill_case(device, code, h, kvh, d, bs, prior, qlens, seed, causal=True, n
     q = random_words(rng, (int(qlens.sum()), h, d), code)
     cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.uint32)
     lens32 = lens.astype(np.uint32)
-    scale = d ** -0.5
+    scale = d ** -0.5 if scale is None else scale
     out = vpa.paged_attention_varlen_prefill(
         to_dev(q, code, device), to_dev(kc, code, device), to_dev(vc, code, device),
         u32(bt, device), u32(lens32, device), u32(cu, device), None, None, scale, 1.0,
@@ -77,6 +77,16 @@ def test_prefill_head_dims_and_groups(device, d, h, kvh):
     got, want = prefill_case(device, orc.BF16, h, kvh, d, 16, [7, 0, 260], [40, 65, 17],
                              seed=d + h + kvh)
     assert_attention_close(got, want, orc.BF16, f"d={d} h={h} kvh={kvh}")
+
+
+@pytest.mark.parametrize("scale", [-0.125, 1.0, 4.0])
+def test_prefill_softmax_scales(device, scale):
+    """Scales far from 1/sqrt(D): large ones spread a row's scores over many
+    binades, so the running max moves often and the deferred rescale of O
+    runs on most tiles; a negative scale flips which key dominates."""
+    got, want = prefill_case(device, orc.BF16, 16, 8, 128, 16, [300, 0, 45], [90, 200, 1],
+                             seed=int(scale * 8) + 40, scale=scale)
+    assert_attention_close(got, want, orc.BF16, f"scale={scale}")
 
 
 def test_prefill_without_prior_is_plain_causal_attention(device):
