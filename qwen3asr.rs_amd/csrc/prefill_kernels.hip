@@ -130,6 +130,34 @@ __device__ __forceinline__ v4i_t lds_read_b128(uint32_t addr) {
   return r;
 }
 
+// dst[i] = 16 bytes at addr + i * STRIDE (+ SECOND for dst2), i < N
+template <int STRIDE, int... I>
+__device__ __forceinline__ void lds_read_seq(v4i_t* dst, uint32_t addr,
+                                             std::integer_sequence<int, I...>) {
+  ((dst[I] = lds_read_b128<I * STRIDE>(addr)), ...);
+}
+template <int STRIDE, int SECOND, int... I>
+__device__ __forceinline__ void lds_read_pairs(v4i_t (*dst)[2], uint32_t addr,
+                                               std::integer_sequence<int, I...>) {
+  ((dst[I][0] = lds_read_b128<I * STRIDE>(addr),
+    dst[I][1] = lds_read_b128<I * STRIDE + SECOND>(addr)),
+   ...);
+}
+
+// S^T = K . Q^T of one tile: KS chained MFMAs over the head dimension
+template <typename T, int KS>
+__device__ __forceinline__ f32x16_t s_tile_mfma(const v4i_t* kop, const uint4* qop) {
+  f32x16_t acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const v4i_t k = kop[ks];
+    acc = mfma32x32x16<T>(make_uint4(k[0], k[1], k[2], k[3]), qop[ks], acc);
+  }
+  return acc;
+}
+
 // Key held in row i of the S^T tile: bits 2 and 3 of i swapped. Lane half h
 // of the 32x32 accumulator holds rows {4h..4h+3, 8+4h..8+4h+3} of every 16;
 // through this order those rows are keys 8h..8h+7, one whole 16-byte unit of
@@ -309,14 +337,12 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   constexpr int kVStep1 = ((2 / UB) * RBV + (2 % UB) * D) * 16;
   const uint32_t va_lane = (uint32_t)((vgroup(half) + col) * 16);
 
-  auto compute = [&](auto sc, int t) {
+  // keys of tile t that exist: inside the context and in a present block
+  // (uniform over the workgroup)
+  auto tile_mask = [&](int t) {
     const int k0 = t * KT;
-    if (k0 >= wave_keys) return;  // no row of this wave sees these keys
-    const uint4* sk = kst(sc);
-    const uint4* sv = vst(sc);
     uint32_t pb[NBT];
     tile_blocks(k0, pb);
-    // keys of the tile that exist: inside the context and in a present block
     uint32_t vmask = 0;
 #pragma unroll
     for (int kb = 0; kb < NBT; ++kb)
@@ -324,14 +350,32 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
         vmask |= (BS >= 32 ? 0xffffffffu : ((1u << BS) - 1u)) << (kb * BS);
     const int nk = k_len - k0;
     if (nk < KT) vmask &= (1u << max(nk, 0)) - 1u;
+    return vmask;
+  };
+
+  // Zero the LDS values of the keys vmask leaves out: their slots hold
+  // stale data (maybe NaN), and a zero probability times NaN would poison O.
+  // Element k % 8 of unit (k / 8, d) holds key k of dim d.
+  auto zero_absent_values = [&](auto sc, uint32_t vmask) {
+    uint16_t* v16 = reinterpret_cast<uint16_t*>(vst(sc));
+    const uint32_t absent = ~vmask;
+    for (int e = tid; e < KT * D; e += kPrefillThreads) {
+      const int k = e / D, d = e % D;
+      if ((absent >> k) & 1u) v16[(vgroup(k / 8) + d) * X + k % 8] = 0;
+    }
+  };
+
+  auto compute = [&](auto sc, int t, uint32_t vmask) {
+    const int k0 = t * KT;
+    if (k0 >= wave_keys) return;  // no row of this wave sees these keys
+    const uint4* sk = kst(sc);
+    const uint4* sv = vst(sc);
     const bool full = vmask == 0xffffffffu && k0 + KT - 1 <= wave_min_limit;
 
     // S^T = K . Q^T; the K operand of k-step ks is chunk 2 ks + half of the
     // key in row col
     v4i_t kop[KS];
-    [&]<int... I>(std::integer_sequence<int, I...>) {
-      ((kop[I] = lds_read_b128<I * 2 * BS * 16>(ka_lane + lds_addr(sk))), ...);
-    }(std::make_integer_sequence<int, KS>{});
+    lds_read_seq<2 * BS * 16>(kop, ka_lane + lds_addr(sk), std::make_integer_sequence<int, KS>{});
     if constexpr (KS == 8) {
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kop[0]), "+v"(kop[1]), "+v"(kop[2]),
                    "+v"(kop[3]), "+v"(kop[4]), "+v"(kop[5]), "+v"(kop[6]), "+v"(kop[7]));
@@ -340,32 +384,21 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kop[0]), "+v"(kop[1]), "+v"(kop[2]),
                    "+v"(kop[3]));
     }
-    f32x16_t sacc;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      sacc = mfma32x32x16<T>(__builtin_bit_cast(uint4, kop[ks]), qop[ks], sacc);
+    f32x16_t sacc = s_tile_mfma<T, KS>(kop, qop);
 
     // online softmax of the row on the raw scores (the scale is positive);
     // P^T operands straight from the accumulator
-    float sval[16];
-    float mx = -INFINITY;
-    if (full) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sval[r] = sacc[r];
-        mx = fmaxf(mx, sval[r]);
-      }
-    } else {
+    if (!full) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = 16 * (r / 8) + 8 * half + r % 8;  // key of element r
         const bool ok = ((vmask >> key) & 1u) && k0 + key <= limit;
-        sval[r] = ok ? sacc[r] : -INFINITY;
-        mx = fmaxf(mx, sval[r]);
+        sacc[r] = ok ? sacc[r] : -INFINITY;
       }
     }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
     mx = max_xor32(mx) * sl;
     // The reference max m only moves when some row's tile max exceeds it by
     // more than kRescaleSlack (log2 units): the probabilities stay below
@@ -382,10 +415,11 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
       m = m_new;
     }
     const float m_use = m == -INFINITY ? 0.f : m;  // a row without keys so far
+    float sval[16];
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      sval[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sval[r], sl, -m_use));
+      sval[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], sl, -m_use));
       ps += sval[r];
     }
     lsum += ps;
@@ -396,20 +430,11 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
                           pack2_hw<T>(sval[8 * k2 + 2], sval[8 * k2 + 3]),
                           pack2_hw<T>(sval[8 * k2 + 4], sval[8 * k2 + 5]),
                           pack2_hw<T>(sval[8 * k2 + 6], sval[8 * k2 + 7]));
-    // per-key 16-bit masks of the V operands: values of keys that do not
-    // exist are zeroed (stale slots may hold NaN, and 0 * NaN poisons O)
-    auto keymask2 = [&](int key) {
-      const uint32_t b = (vmask >> key) & 3u;
-      return ((b & 1u) ? 0x0000ffffu : 0u) | ((b & 2u) ? 0xffff0000u : 0u);
-    };
-
     // O^T += V^T . P^T: k-step k2 of lane half h covers keys 16 k2 + 8h ..
-    // 16 k2 + 8h + 7, one unit of row d = 32 dt + col
+    // 16 k2 + 8h + 7, one unit of row d = 32 dt + col (values of absent keys
+    // were zeroed in LDS by the step)
     v4i_t vop[DT][2];
-    [&]<int... I>(std::integer_sequence<int, I...>) {
-      ((vop[I][0] = lds_read_b128<I * 32 * 16>(va_lane + lds_addr(sv)),
-        vop[I][1] = lds_read_b128<I * 32 * 16 + kVStep1>(va_lane + lds_addr(sv))), ...);
-    }(std::make_integer_sequence<int, DT>{});
+    lds_read_pairs<32 * 16, kVStep1>(vop, va_lane + lds_addr(sv), std::make_integer_sequence<int, DT>{});
     if constexpr (DT == 4) {
       asm volatile("s_waitcnt lgkmcnt(0)"
                    : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[1][0]), "+v"(vop[1][1]),
@@ -418,21 +443,6 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
       static_assert(DT == 2, "head_dim 64 or 128");
       asm volatile("s_waitcnt lgkmcnt(0)"
                    : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[1][0]), "+v"(vop[1][1]));
-    }
-    if (vmask != 0xffffffffu) {
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        const int kl = 16 * k2 + 8 * half;
-        const uint32_t m0 = keymask2(kl), m1 = keymask2(kl + 2), m2 = keymask2(kl + 4),
-                       m3 = keymask2(kl + 6);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          vop[dt][k2][0] &= m0;
-          vop[dt][k2][1] &= m1;
-          vop[dt][k2][2] &= m2;
-          vop[dt][k2][3] &= m3;
-        }
-      }
     }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -457,10 +467,16 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    const uint32_t vmask = tile_mask(t);
+    if (vmask != 0xffffffffu) {  // rare: the sequence's last tile, absent blocks
+      zero_absent_values(sc, vmask);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
     if (t + NS - 1 < n_tiles) issue(Int<(S + NS - 1) % NS>{}, t + NS - 1);
-    compute(sc, t);
+    compute(sc, t, vmask);
   };
-
   if (n_tiles > 0) {
     issue(Int<0>{}, 0);
     if (NS > 2 && 1 < n_tiles) issue(Int<1 % NS>{}, 1);
