@@ -11,7 +11,11 @@ the header of ``vpa_oracle.c``. In short: the paged cache layout of
 ``repeat_kv`` (``vasr-models/src/model/attention.rs:12-21``), eager softmax
 attention (``attention.rs:243-286``), cached causal mask
 (``attention.rs:78-149``) and the ``+1e-6`` softmax denominator of the paged
-sibling kernel (``prefill_paged_attn.metal:1300``).
+sibling kernel (``prefill_paged_attn.metal:1300``). FP8 (E4M3FN) caches:
+decode as ``prefill_paged_attn.metal:698-722``, dequantisation
+``(float)byte * scale`` rounded to the query type (``:764-769``), and the
+published quantising rule of the un-vendored kernels, round-to-nearest-even
+of ``x / scale`` saturating at 448.
 """
 
 from __future__ import annotations
@@ -22,7 +26,7 @@ import subprocess
 
 import numpy as np
 
-F32, F16, BF16 = 0, 1, 2
+F32, F16, BF16, FP8 = 0, 1, 2, 3
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libvpa_oracle.so")
@@ -55,6 +59,25 @@ def lib():
         L.oracle_paged_attention_f64.argtypes = [_i32, _p, _p, _p, _p, _p, _i32, _p, _i32, _dbl,
                                                  _i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64]
         L.oracle_paged_attention_f64.restype = None
+        L.oracle_fp8_to_f32_array.argtypes = [_p, _p, _i64]
+        L.oracle_fp8_to_f32_array.restype = None
+        L.oracle_fp8_from_f32_array.argtypes = [_p, _p, _i64]
+        L.oracle_fp8_from_f32_array.restype = None
+        L.oracle_reshape_and_cache_fp8.argtypes = [_i32, _p, _p, _i64, _i64, _p, _p, _p, _i64,
+                                                   _i32, _i32, _i32, _i64, _i64, _i64, _flt,
+                                                   _flt]
+        L.oracle_reshape_and_cache_fp8.restype = None
+        L.oracle_gather_kv_cache_fp8.argtypes = [_i32, _p, _p, _p, _p, _p, _i32, _p, _i32, _i32,
+                                                 _i32, _i32, _i64, _i64, _i64, _flt, _flt]
+        L.oracle_gather_kv_cache_fp8.restype = None
+        L.oracle_paged_attention_kv_f64.argtypes = [_i32, _i32, _flt, _flt, _p, _p, _p, _p, _p,
+                                                    _i32, _p, _i32, _dbl, _i32, _i32, _i32, _i32,
+                                                    _i32, _i64, _i64, _i64]
+        L.oracle_paged_attention_kv_f64.restype = None
+        L.oracle_prefill_attention_kv_f64.argtypes = [_i32, _i32, _flt, _flt, _p, _p, _p, _p, _p,
+                                                      _i32, _p, _p, _i32, _i32, _dbl, _i32, _i32,
+                                                      _i32, _i32, _i64, _i64, _i64, _dbl]
+        L.oracle_prefill_attention_kv_f64.restype = None
         L.oracle_prefill_attention_f64.argtypes = [_i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i32,
                                                    _i32, _dbl, _i32, _i32, _i32, _i32, _i64,
                                                    _i64, _i64, _dbl]
@@ -112,23 +135,27 @@ def gather_kv_cache(key_cache, value_cache, block_tables, cu_seqlens, dtype=None
 
 
 def paged_attention(q, key_cache, value_cache, block_tables, context_lens, max_context_len,
-                    scale, dtype=None) -> np.ndarray:
-    """Decode attention, float64 result [B, H, D]."""
+                    scale, dtype=None, kv_dtype=None, k_scale=1.0, v_scale=1.0) -> np.ndarray:
+    """Decode attention, float64 result [B, H, D]. ``kv_dtype=FP8`` reads an
+    fp8 cache (uint8 arrays) dequantised with ``k_scale`` / ``v_scale``."""
     code = dtype_code(q, dtype)
+    kv = code if kv_dtype is None else kv_dtype
     nb, kvh, d, bs, bstride, hstride = _cache_geom(key_cache)
     b, h, _ = q.shape
     block_tables = np.ascontiguousarray(block_tables, dtype=np.uint32)
     context_lens = np.ascontiguousarray(context_lens, dtype=np.uint32)
     out = np.zeros((b, h, d), dtype=np.float64)
-    lib().oracle_paged_attention_f64(code, _ptr(out), _ptr(q), _ptr(key_cache), _ptr(value_cache),
-                                     _ptr(block_tables), block_tables.shape[1], _ptr(context_lens),
-                                     int(max_context_len), float(scale), b, h, kvh, d, bs, nb,
-                                     bstride, hstride)
+    lib().oracle_paged_attention_kv_f64(code, kv, float(k_scale), float(v_scale), _ptr(out),
+                                        _ptr(q), _ptr(key_cache), _ptr(value_cache),
+                                        _ptr(block_tables), block_tables.shape[1],
+                                        _ptr(context_lens), int(max_context_len), float(scale), b,
+                                        h, kvh, d, bs, nb, bstride, hstride)
     return out
 
 
 def prefill_attention(q, key_cache, value_cache, block_tables, context_lens, cu_seqlens_q, scale,
-                      causal=True, dtype=None, eps=0.0) -> np.ndarray:
+                      causal=True, dtype=None, eps=0.0, kv_dtype=None, k_scale=1.0,
+                      v_scale=1.0) -> np.ndarray:
     """Chunked prefill attention over the paged cache, float64 [total_q, H, D].
 
     ``eps`` is added to the softmax denominator: 0.0 is the flash varlen path
@@ -141,12 +168,60 @@ def prefill_attention(q, key_cache, value_cache, block_tables, context_lens, cu_
     context_lens = np.ascontiguousarray(context_lens, dtype=np.uint32)
     cu_seqlens_q = np.ascontiguousarray(cu_seqlens_q, dtype=np.uint32)
     out = np.zeros((tq, h, d), dtype=np.float64)
-    lib().oracle_prefill_attention_f64(code, _ptr(out), _ptr(q), _ptr(key_cache),
-                                       _ptr(value_cache), _ptr(block_tables), block_tables.shape[1],
-                                       _ptr(context_lens), _ptr(cu_seqlens_q),
-                                       block_tables.shape[0], int(bool(causal)), float(scale), h,
-                                       kvh, d, bs, nb, bstride, hstride, float(eps))
+    kv = code if kv_dtype is None else kv_dtype
+    lib().oracle_prefill_attention_kv_f64(code, kv, float(k_scale), float(v_scale), _ptr(out),
+                                          _ptr(q), _ptr(key_cache), _ptr(value_cache),
+                                          _ptr(block_tables), block_tables.shape[1],
+                                          _ptr(context_lens), _ptr(cu_seqlens_q),
+                                          block_tables.shape[0], int(bool(causal)), float(scale),
+                                          h, kvh, d, bs, nb, bstride, hstride, float(eps))
     return out
+
+
+def fp8_to_f32(b: np.ndarray) -> np.ndarray:
+    """E4M3FN bytes -> float32 (exact)."""
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.empty(b.shape, dtype=np.float32)
+    lib().oracle_fp8_to_f32_array(_ptr(b), _ptr(out), b.size)
+    return out
+
+
+def fp8_from_f32(x: np.ndarray) -> np.ndarray:
+    """float32 -> E4M3FN bytes (round to nearest even, saturate at 448)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8)
+    lib().oracle_fp8_from_f32_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def reshape_and_cache_fp8(key, value, key_cache, value_cache, slot_mapping, dtype, k_scale,
+                          v_scale):
+    """In-place append of key/value rows [T, KVH, D] (dtype code ``dtype``)
+    into uint8 fp8 caches [NB, KVH, D/16, BS, 16] / [NB, KVH, D, BS]."""
+    nb, kvh, d, bs, bstride, hstride = _cache_geom(key_cache)
+    t = key.shape[0]
+    slot_mapping = np.ascontiguousarray(slot_mapping, dtype=np.int64)
+    lib().oracle_reshape_and_cache_fp8(dtype, _ptr(key), _ptr(value), kvh * d, kvh * d,
+                                       _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping), t,
+                                       kvh, d, bs, nb, bstride, hstride, float(k_scale),
+                                       float(v_scale))
+
+
+def gather_kv_cache_fp8(key_cache, value_cache, block_tables, cu_seqlens, out_dtype, k_scale,
+                        v_scale):
+    """Packed dequantised rows [rows, KVH, D] of ``out_dtype`` (code) from fp8 caches."""
+    nb, kvh, d, bs, bstride, hstride = _cache_geom(key_cache)
+    block_tables = np.ascontiguousarray(block_tables, dtype=np.uint32)
+    cu_seqlens = np.ascontiguousarray(cu_seqlens, dtype=np.uint32)
+    rows = int(cu_seqlens[-1])
+    npdt = np.float32 if out_dtype == F32 else np.uint16
+    ok = np.zeros((rows, kvh, d), dtype=npdt)
+    ov = np.zeros((rows, kvh, d), dtype=npdt)
+    lib().oracle_gather_kv_cache_fp8(out_dtype, _ptr(ok), _ptr(ov), _ptr(key_cache),
+                                     _ptr(value_cache), _ptr(block_tables), block_tables.shape[1],
+                                     _ptr(cu_seqlens), block_tables.shape[0], kvh, d, bs, nb,
+                                     bstride, hstride, float(k_scale), float(v_scale))
+    return ok, ov
 
 
 def cpu_baseline_decode_step(q, new_key, new_value, slot_mapping, key_cache, value_cache,

@@ -29,8 +29,20 @@
  * the reference's CPU path restated in f32 with OpenMP over (seq, kv head)
  * for timing only.
  *
- * Element types: 0 = f32, 1 = f16, 2 = bf16 (same codes as include/vpa.h).
- * 16-bit elements are raw uint16_t words.
+ * Element types: 0 = f32, 1 = f16, 2 = bf16, 3 = fp8 E4M3FN (cache only;
+ * same codes as include/vpa.h). 16-bit elements are raw uint16_t words, fp8
+ * elements raw bytes.
+ *
+ * FP8 cache (the reference's uint8 cache variant): decode of a byte follows
+ * the E4M3FN format the reference's Metal kernels read
+ * (vasr-paged-attn/src/metal/kernels/prefill_paged_attn.metal:698-722), and a
+ * cached value is dequantised as (float)byte * scale rounded to the query
+ * type (:764-769). The quantising side, reshape_and_cache into an fp8 cache,
+ * lives in the un-vendored mistralrs-paged-attn crate; its published rule
+ * (the vLLM kernels it derives from) is byte = E4M3FN(x / scale) with
+ * round-to-nearest-even and saturation to the largest finite value (448),
+ * NaN staying NaN. Both directions are pinned in tests/test_oracle.py
+ * against torch.float8_e4m3fn and the format's closed forms.
  */
 #include <math.h>
 #include <stdint.h>
@@ -43,8 +55,96 @@
 #define ORC_F32 0
 #define ORC_F16 1
 #define ORC_BF16 2
+#define ORC_FP8 3
 
-static int elem_bytes(int dtype) { return dtype == ORC_F32 ? 4 : 2; }
+static int elem_bytes(int dtype) { return dtype == ORC_F32 ? 4 : (dtype == ORC_FP8 ? 1 : 2); }
+
+static uint32_t f32_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static float bits_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* E4M3FN byte -> binary32, exact: bias 7, no infinities, S.1111.111 = NaN,
+ * exponent field 0 = subnormal m * 2^-9. */
+float oracle_fp8_to_f32(uint8_t v) {
+  const uint32_t sign = (uint32_t)(v & 0x80) << 24;
+  const uint32_t e = (v >> 3) & 0xf, m = v & 7;
+  if (e == 0xf && m == 7) return bits_f32(sign | 0x7fc00000u);
+  if (e == 0) {
+    const float mag = (float)m * 0x1p-9f;
+    return (v & 0x80) ? -mag : mag;
+  }
+  return bits_f32(sign | ((e + 120) << 23) | (m << 20));
+}
+
+/* binary32 -> E4M3FN byte: round to nearest, ties to even; |x| >= 448 (and
+ * infinities) saturate to +-448; NaN gives S.1111.111. */
+uint8_t oracle_fp8_from_f32(float x) {
+  const uint32_t u = f32_bits(x);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7f;  /* NaN */
+  if (a >= 0x43e00000u) return sign | 0x7e; /* >= 448: largest finite */
+  if (a < 0x3c800000u) {                    /* below 2^-6: multiples of 2^-9 */
+    const float t = bits_f32(a) * 512.0f;   /* exact */
+    float r = floorf(t);
+    const float frac = t - r;
+    if (frac > 0.5f || (frac == 0.5f && fmodf(r, 2.0f) == 1.0f)) r += 1.0f;
+    return sign | (uint8_t)r;                /* r == 8 is 2^-6, the first normal */
+  }
+  const uint32_t lsb = (a >> 20) & 1;
+  const uint32_t r = a + 0x7ffffu + lsb;    /* round the 23-bit mantissa to 3 bits */
+  const uint32_t e = (r >> 23) - 120, m = (r >> 20) & 7;
+  return sign | (uint8_t)((e << 3) | m);
+}
+
+void oracle_fp8_to_f32_array(const uint8_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_fp8_to_f32(in[i]);
+}
+void oracle_fp8_from_f32_array(const float* in, uint8_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_fp8_from_f32(in[i]);
+}
+
+/* binary32 -> bf16 / binary16 words, round to nearest even (NaN kept). */
+static uint16_t f32_to_bf16_rne(float f) {
+  const uint32_t u = f32_bits(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1)) >> 16);
+}
+static uint16_t f32_to_f16_rne(float f) {
+  const uint32_t u = f32_bits(f);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7e00;                   /* NaN */
+  if (a >= 0x477ff000u) return sign | 0x7c00;                  /* rounds past 65504: inf */
+  if (a < 0x38800000u) {                                       /* below 2^-14: subnormal */
+    const double t = (double)bits_f32(a) * 16777216.0;          /* units of 2^-24, exact */
+    double r = floor(t);
+    const double frac = t - r;
+    if (frac > 0.5 || (frac == 0.5 && fmod(r, 2.0) == 1.0)) r += 1.0;
+    return sign | (uint16_t)r;
+  }
+  const uint32_t r = a + 0xfffu + ((a >> 13) & 1);
+  return sign | (uint16_t)((((r >> 23) - 112) << 10) | ((r >> 13) & 0x3ff));
+}
+static float round_to(int dtype, float f) {
+  if (dtype == ORC_BF16) return bits_f32((uint32_t)f32_to_bf16_rne(f) << 16);
+  if (dtype == ORC_F16) {
+    const uint16_t h = f32_to_f16_rne(f);
+    /* widen back exactly */
+    const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    if (e == 0) return (sign ? -1.0f : 1.0f) * (float)m * 0x1p-24f;
+    if (e == 31) return bits_f32(sign | 0x7f800000u | (m << 13));
+    return bits_f32(sign | ((e + 112) << 23) | (m << 13));
+  }
+  return f;
+}
 
 static float bf16_to_f32(uint16_t h) {
   uint32_t u = (uint32_t)h << 16;
@@ -182,12 +282,21 @@ void oracle_gather_kv_cache(int dtype, void* out_key, void* out_value, const voi
  * `logits` is caller scratch of n_keys doubles. Returns 0 if no token is
  * valid (out = 0).
  */
-static void attend_row_f64(int dtype, double* out, const void* q, int64_t q_off,
-                           const void* key_cache, const void* value_cache,
-                           const uint32_t* bt_row, int64_t n_keys, int head, int head_dim,
-                           int block_size, int64_t num_blocks, int64_t block_stride,
-                           int64_t head_stride, double scale, double eps, double* logits) {
-  const int x = 16 / elem_bytes(dtype);
+/* One cached K or V element as the attention reads it: the element itself
+ * for 16/32-bit caches; for an fp8 cache (float)byte * scale rounded to the
+ * query type (prefill_paged_attn.metal:764-769). */
+static double load_cache(int kv_dtype, int q_dtype, const void* base, int64_t idx, float scale) {
+  if (kv_dtype != ORC_FP8) return load_elem(base, kv_dtype, idx);
+  return (double)round_to(q_dtype, oracle_fp8_to_f32(((const uint8_t*)base)[idx]) * scale);
+}
+
+static void attend_row_f64(int dtype, int kv_dtype, float k_scale, float v_scale, double* out,
+                           const void* q, int64_t q_off, const void* key_cache,
+                           const void* value_cache, const uint32_t* bt_row, int64_t n_keys,
+                           int head, int head_dim, int block_size, int64_t num_blocks,
+                           int64_t block_stride, int64_t head_stride, double scale, double eps,
+                           double* logits) {
+  const int x = 16 / elem_bytes(kv_dtype);
   double m = -INFINITY;
   for (int64_t t = 0; t < n_keys; ++t) {
     const uint32_t blk = bt_row[t / block_size];
@@ -199,8 +308,9 @@ static void attend_row_f64(int dtype, double* out, const void* q, int64_t q_off,
     double acc = 0.0;
     for (int d = 0; d < head_dim; ++d)
       acc += load_elem(q, dtype, q_off + d) *
-             load_elem(key_cache, dtype,
-                       key_index(blk, head, d, off, block_size, x, block_stride, head_stride));
+             load_cache(kv_dtype, dtype, key_cache,
+                        key_index(blk, head, d, off, block_size, x, block_stride, head_stride),
+                        k_scale);
     logits[t] = acc * scale;
     if (logits[t] > m) m = logits[t];
   }
@@ -214,9 +324,10 @@ static void attend_row_f64(int dtype, double* out, const void* q, int64_t q_off,
     const uint32_t blk = bt_row[t / block_size];
     const int off = (int)(t % block_size);
     for (int d = 0; d < head_dim; ++d)
-      out[d] += p * load_elem(value_cache, dtype,
-                              value_index(blk, head, d, off, block_size, block_stride,
-                                          head_stride));
+      out[d] += p * load_cache(kv_dtype, dtype, value_cache,
+                               value_index(blk, head, d, off, block_size, block_stride,
+                                           head_stride),
+                               v_scale);
   }
   const double inv = 1.0 / (sum + eps);
   for (int d = 0; d < head_dim; ++d) out[d] *= inv;
@@ -227,13 +338,14 @@ static void attend_row_f64(int dtype, double* out, const void* q, int64_t q_off,
  * L = min(context_lens[s], max_context_len, block_table_stride * BS);
  * kv head of q head h is h / (H / KVH).
  */
-void oracle_paged_attention_f64(int dtype, double* out, const void* query,
-                                const void* key_cache, const void* value_cache,
-                                const uint32_t* block_tables, int block_table_stride,
-                                const uint32_t* context_lens, int max_context_len, double scale,
-                                int num_seqs, int num_heads, int num_kv_heads, int head_dim,
-                                int block_size, int64_t num_blocks, int64_t block_stride,
-                                int64_t head_stride) {
+void oracle_paged_attention_kv_f64(int dtype, int kv_dtype, float k_scale, float v_scale,
+                                   double* out, const void* query, const void* key_cache,
+                                   const void* value_cache, const uint32_t* block_tables,
+                                   int block_table_stride, const uint32_t* context_lens,
+                                   int max_context_len, double scale, int num_seqs,
+                                   int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                   int64_t num_blocks, int64_t block_stride,
+                                   int64_t head_stride) {
   const int group = num_heads / num_kv_heads;
 #pragma omp parallel
   {
@@ -251,7 +363,8 @@ void oracle_paged_attention_f64(int dtype, double* out, const void* query,
           cap = L;
           logits = (double*)malloc(sizeof(double) * (size_t)cap);
         }
-        attend_row_f64(dtype, out + ((int64_t)s * num_heads + h) * head_dim, query,
+        attend_row_f64(dtype, kv_dtype, k_scale, v_scale,
+                       out + ((int64_t)s * num_heads + h) * head_dim, query,
                        ((int64_t)s * num_heads + h) * head_dim, key_cache, value_cache,
                        block_tables + (int64_t)s * block_table_stride, L, h / group, head_dim,
                        block_size, num_blocks, block_stride, head_stride, scale, 1e-6, logits);
@@ -259,6 +372,19 @@ void oracle_paged_attention_f64(int dtype, double* out, const void* query,
     }
     free(logits);
   }
+}
+
+void oracle_paged_attention_f64(int dtype, double* out, const void* query,
+                                const void* key_cache, const void* value_cache,
+                                const uint32_t* block_tables, int block_table_stride,
+                                const uint32_t* context_lens, int max_context_len, double scale,
+                                int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                                int block_size, int64_t num_blocks, int64_t block_stride,
+                                int64_t head_stride) {
+  oracle_paged_attention_kv_f64(dtype, dtype, 1.0f, 1.0f, out, query, key_cache, value_cache,
+                                block_tables, block_table_stride, context_lens, max_context_len,
+                                scale, num_seqs, num_heads, num_kv_heads, head_dim, block_size,
+                                num_blocks, block_stride, head_stride);
 }
 
 /*
@@ -271,14 +397,14 @@ void oracle_paged_attention_f64(int dtype, double* out, const void* query,
  * The softmax denominator is sum + eps: 0 for the flash varlen path the CUDA
  * build takes (attention.rs:554-664), 1e-6 for the Metal kernel (:1300).
  */
-void oracle_prefill_attention_f64(int dtype, double* out, const void* query,
-                                  const void* key_cache, const void* value_cache,
-                                  const uint32_t* block_tables, int block_table_stride,
-                                  const uint32_t* context_lens, const uint32_t* cu_seqlens_q,
-                                  int num_seqs, int causal, double scale, int num_heads,
-                                  int num_kv_heads, int head_dim, int block_size,
-                                  int64_t num_blocks, int64_t block_stride,
-                                  int64_t head_stride, double eps) {
+void oracle_prefill_attention_kv_f64(int dtype, int kv_dtype, float k_scale, float v_scale,
+                                     double* out, const void* query, const void* key_cache,
+                                     const void* value_cache, const uint32_t* block_tables,
+                                     int block_table_stride, const uint32_t* context_lens,
+                                     const uint32_t* cu_seqlens_q, int num_seqs, int causal,
+                                     double scale, int num_heads, int num_kv_heads,
+                                     int head_dim, int block_size, int64_t num_blocks,
+                                     int64_t block_stride, int64_t head_stride, double eps) {
   const int group = num_heads / num_kv_heads;
   for (int s = 0; s < num_seqs; ++s) {
     const int64_t n = (int64_t)cu_seqlens_q[s + 1] - cu_seqlens_q[s];
@@ -294,7 +420,7 @@ void oracle_prefill_attention_f64(int dtype, double* out, const void* query,
           int64_t nk = causal ? P + i + 1 : L;
           if (nk > L) nk = L;
           if (nk < 0) nk = 0;
-          attend_row_f64(dtype, out + (row * num_heads + h) * head_dim, query,
+          attend_row_f64(dtype, kv_dtype, k_scale, v_scale, out + (row * num_heads + h) * head_dim, query,
                          (row * num_heads + h) * head_dim, key_cache, value_cache,
                          block_tables + (int64_t)s * block_table_stride, nk, h / group,
                          head_dim, block_size, num_blocks, block_stride, head_stride, scale, eps,
@@ -302,6 +428,97 @@ void oracle_prefill_attention_f64(int dtype, double* out, const void* query,
         }
       }
       free(logits);
+    }
+  }
+}
+
+void oracle_prefill_attention_f64(int dtype, double* out, const void* query,
+                                  const void* key_cache, const void* value_cache,
+                                  const uint32_t* block_tables, int block_table_stride,
+                                  const uint32_t* context_lens, const uint32_t* cu_seqlens_q,
+                                  int num_seqs, int causal, double scale, int num_heads,
+                                  int num_kv_heads, int head_dim, int block_size,
+                                  int64_t num_blocks, int64_t block_stride,
+                                  int64_t head_stride, double eps) {
+  oracle_prefill_attention_kv_f64(dtype, dtype, 1.0f, 1.0f, out, query, key_cache, value_cache,
+                                  block_tables, block_table_stride, context_lens, cu_seqlens_q,
+                                  num_seqs, causal, scale, num_heads, num_kv_heads, head_dim,
+                                  block_size, num_blocks, block_stride, head_stride, eps);
+}
+
+/*
+ * reshape_and_cache into an fp8 cache: key/value rows of dtype `dtype`
+ * ([T, KVH, D] with token strides), byte = fp8(x / scale) (see the file
+ * header), layout as above with x = 16.
+ */
+void oracle_reshape_and_cache_fp8(int dtype, const void* key, const void* value,
+                                  int64_t key_token_stride, int64_t value_token_stride,
+                                  uint8_t* key_cache, uint8_t* value_cache,
+                                  const int64_t* slot_mapping, int64_t num_tokens,
+                                  int num_kv_heads, int head_dim, int block_size,
+                                  int64_t num_blocks, int64_t block_stride, int64_t head_stride,
+                                  float k_scale, float v_scale) {
+  for (int64_t t = 0; t < num_tokens; ++t) {
+    const int64_t s = slot_mapping[t];
+    if (s < 0 || s >= num_blocks * block_size) continue;
+    const int64_t blk = s / block_size;
+    const int off = (int)(s % block_size);
+    for (int j = 0; j < num_kv_heads; ++j) {
+      for (int d = 0; d < head_dim; ++d) {
+        const float k = load_f32(key, dtype, t * key_token_stride + (int64_t)j * head_dim + d);
+        const float v =
+            load_f32(value, dtype, t * value_token_stride + (int64_t)j * head_dim + d);
+        key_cache[key_index(blk, j, d, off, block_size, 16, block_stride, head_stride)] =
+            oracle_fp8_from_f32(k / k_scale);
+        value_cache[value_index(blk, j, d, off, block_size, block_stride, head_stride)] =
+            oracle_fp8_from_f32(v / v_scale);
+      }
+    }
+  }
+}
+
+/*
+ * gather_kv_cache from an fp8 cache: like oracle_gather_kv_cache, each value
+ * dequantised to (float)byte * scale and stored as out_dtype (round to
+ * nearest even); absent blocks give zero rows.
+ */
+void oracle_gather_kv_cache_fp8(int out_dtype, void* out_key, void* out_value,
+                                const uint8_t* key_cache, const uint8_t* value_cache,
+                                const uint32_t* block_tables, int block_table_stride,
+                                const uint32_t* cu_seqlens, int num_seqs, int num_kv_heads,
+                                int head_dim, int block_size, int64_t num_blocks,
+                                int64_t block_stride, int64_t head_stride, float k_scale,
+                                float v_scale) {
+  const int eb = elem_bytes(out_dtype);
+  for (int s = 0; s < num_seqs; ++s) {
+    const int64_t len = (int64_t)cu_seqlens[s + 1] - cu_seqlens[s];
+    for (int64_t t = 0; t < len; ++t) {
+      const uint32_t blk = block_tables[(int64_t)s * block_table_stride + t / block_size];
+      const int off = (int)(t % block_size);
+      const int64_t row = (int64_t)cu_seqlens[s] + t;
+      for (int j = 0; j < num_kv_heads; ++j) {
+        for (int d = 0; d < head_dim; ++d) {
+          const int64_t o = (row * num_kv_heads + j) * head_dim + d;
+          float kf = 0.0f, vf = 0.0f;
+          if ((int64_t)blk < num_blocks) {
+            kf = oracle_fp8_to_f32(key_cache[key_index(blk, j, d, off, block_size, 16,
+                                                       block_stride, head_stride)]) * k_scale;
+            vf = oracle_fp8_to_f32(value_cache[value_index(blk, j, d, off, block_size,
+                                                           block_stride, head_stride)]) * v_scale;
+          }
+          if (out_dtype == ORC_F32) {
+            ((float*)out_key)[o] = kf;
+            ((float*)out_value)[o] = vf;
+          } else if (out_dtype == ORC_BF16) {
+            ((uint16_t*)out_key)[o] = f32_to_bf16_rne(kf);
+            ((uint16_t*)out_value)[o] = f32_to_bf16_rne(vf);
+          } else {
+            ((uint16_t*)out_key)[o] = f32_to_f16_rne(kf);
+            ((uint16_t*)out_value)[o] = f32_to_f16_rne(vf);
+          }
+          (void)eb;
+        }
+      }
     }
   }
 }

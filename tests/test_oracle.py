@@ -353,3 +353,115 @@ def test_cpu_baseline_matches_oracle():
     np.testing.assert_array_equal(kc, kc2)
     want = orc.paged_attention(q, kc, vc, bt, lens, int(lens.max()), d ** -0.5, dtype=code)
     np.testing.assert_allclose(out, want, rtol=1e-4, atol=1e-5)
+
+
+# ---- fp8 (E4M3FN) cache ------------------------------------------------------
+
+def test_fp8_decode_of_every_byte_matches_torch():
+    """All 256 E4M3FN codes against torch.float8_e4m3fn, plus the format's
+    closed forms (bias 7, subnormals m * 2^-9, S.1111.111 = NaN)."""
+    codes = np.arange(256, dtype=np.uint8)
+    got = orc.fp8_to_f32(codes)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)])
+    assert got[0x7E] == 448.0 and got[0x38] == 1.0 and got[0x08] == 2.0 ** -6
+    assert got[0x01] == 2.0 ** -9 and np.isnan(got[0x7F]) and np.isnan(got[0xFF])
+    assert got[0x80] == 0.0 and np.signbit(got[0x80])
+
+
+def test_fp8_encode_matches_torch_in_range():
+    """Round to nearest even for every bf16 bit pattern below 448, exact
+    midpoints between neighbouring codes (ties), and random values."""
+    x = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    fin = orc.fp8_to_f32(np.arange(256, dtype=np.uint8))
+    pos = np.sort(np.unique(fin[np.isfinite(fin) & (fin >= 0)]))
+    mids = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
+    rng = np.random.default_rng(7)
+    x = np.concatenate([x, mids, -mids, rng.standard_normal(1 << 20).astype(np.float32) * 40,
+                        rng.random(1 << 18).astype(np.float32) * np.float32(0.03)])
+    x = x[np.isfinite(x) & (np.abs(x) < 448)]
+    got = orc.fp8_from_f32(x)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(got, ref)
+    # ties went to the even code (e.g. 1.0625 is halfway between 1.0 and 1.125)
+    assert orc.fp8_from_f32(np.float32([1.0625, 1.1875]))[0] == 0x38
+    assert orc.fp8_from_f32(np.float32([1.1875]))[0] == 0x3A
+
+
+def test_fp8_encode_saturates_and_keeps_nan():
+    x = np.float32([448.0, 449.0, 464.0, 480.0, 1e6, np.inf, -448.0, -500.0, -np.inf, np.nan])
+    got = orc.fp8_from_f32(x)
+    np.testing.assert_array_equal(got[:6], [0x7E] * 6)
+    np.testing.assert_array_equal(got[6:9], [0xFE] * 3)
+    assert got[9] & 0x7F == 0x7F
+
+
+def test_fp8_encode_decode_idempotent():
+    codes = np.arange(256, dtype=np.uint8)
+    vals = orc.fp8_to_f32(codes)
+    fin = np.isfinite(vals)
+    np.testing.assert_array_equal(orc.fp8_from_f32(vals[fin]), codes[fin])
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F32])
+def test_fp8_append_gather_round_trip(code):
+    """append into an fp8 cache then gather: each value comes back as
+    fp8(x / scale) * scale in the output type; the cache bytes sit where the
+    reference's layout inverse (x = 16) puts them."""
+    rng = np.random.default_rng(31 + code)
+    kvh, d, bs, nb = 2, 64, 16, 24
+    length = 3 * bs + 7
+    table = rng.permutation(nb)[: (length + bs - 1) // bs]
+    kc = np.zeros((nb, kvh, d // 16, bs, 16), dtype=np.uint8)
+    vc = np.zeros((nb, kvh, d, bs), dtype=np.uint8)
+    k = orc.from_f32((rng.standard_normal((length, kvh, d)) * 30).astype(np.float32), code)
+    v = orc.from_f32((rng.standard_normal((length, kvh, d)) * 30).astype(np.float32), code)
+    pos = np.arange(length)
+    slots = table[pos // bs].astype(np.int64) * bs + pos % bs
+    ks, vs = 0.5, 2.0
+    orc.reshape_and_cache_fp8(k, v, kc, vc, slots, code, ks, vs)
+    ki, vi = inverse_layout(kc, vc, table, length)
+    kf = orc.to_f32(k, code) if code != orc.F32 else k
+    vf = orc.to_f32(v, code) if code != orc.F32 else v
+    np.testing.assert_array_equal(ki, orc.fp8_from_f32(kf / np.float32(ks)).transpose(1, 0, 2))
+    np.testing.assert_array_equal(vi, orc.fp8_from_f32(vf / np.float32(vs)).transpose(1, 0, 2))
+    cu = np.array([0, length], dtype=np.uint32)
+    gk, gv = orc.gather_kv_cache_fp8(kc, vc, table[None, :].astype(np.uint32), cu, orc.F32, ks, vs)
+    np.testing.assert_array_equal(gk, orc.fp8_to_f32(ki.transpose(1, 0, 2)) * np.float32(ks))
+    np.testing.assert_array_equal(gv, orc.fp8_to_f32(vi.transpose(1, 0, 2)) * np.float32(vs))
+    gk16, _ = orc.gather_kv_cache_fp8(kc, vc, table[None, :].astype(np.uint32), cu, orc.BF16,
+                                      ks, vs)
+    np.testing.assert_array_equal(gk16, orc.f32_to_bf16_bits(gk))
+
+
+@pytest.mark.parametrize("scales", [(1.0, 1.0), (0.37, 3.1)])
+def test_fp8_attention_equals_attention_over_dequantised_cache(scales):
+    """Decode and prefill over an fp8 cache equal the same attention over a
+    bf16 cache holding bf16(byte * scale), the dequantisation the reference's
+    kernels apply (with scale 1 every E4M3 value is exact in bf16)."""
+    ks, vs = scales
+    rng = np.random.default_rng(5)
+    h, kvh, d, bs, nb = 8, 4, 64, 16, 40
+    kc8 = rng.integers(0, 256, size=(nb, kvh, d // 16, bs, 16), dtype=np.uint8)
+    vc8 = rng.integers(0, 256, size=(nb, kvh, d, bs), dtype=np.uint8)
+    kc8[(kc8 & 0x7F) == 0x7F] = 0x38  # no NaN codes
+    vc8[(vc8 & 0x7F) == 0x7F] = 0x38
+    kdq = orc.f32_to_bf16_bits(orc.fp8_to_f32(kc8) * np.float32(ks))
+    kc16 = np.ascontiguousarray(
+        kdq.reshape(nb, kvh, d // 16, bs, 2, 8).transpose(0, 1, 2, 4, 3, 5).reshape(
+            nb, kvh, d // 8, bs, 8))
+    vc16 = orc.f32_to_bf16_bits(orc.fp8_to_f32(vc8) * np.float32(vs))
+    lens = np.array([1, 40, 129, 300], dtype=np.uint32)
+    bt = np.stack([rng.permutation(nb)[:19] for _ in lens]).astype(np.uint32)
+    q = orc.from_f32(rng.standard_normal((len(lens), h, d)).astype(np.float32), orc.BF16)
+    got = orc.paged_attention(q, kc8, vc8, bt, lens, 304, 0.1, dtype=orc.BF16, kv_dtype=orc.FP8,
+                              k_scale=ks, v_scale=vs)
+    want = orc.paged_attention(q, kc16, vc16, bt, lens, 304, 0.1, dtype=orc.BF16)
+    np.testing.assert_array_equal(got, want)
+    cu = np.array([0, 1, 5, 20, 27], dtype=np.uint32)
+    qp = orc.from_f32(rng.standard_normal((27, h, d)).astype(np.float32), orc.BF16)
+    got = orc.prefill_attention(qp, kc8, vc8, bt, lens, cu, 0.1, dtype=orc.BF16,
+                                kv_dtype=orc.FP8, k_scale=ks, v_scale=vs)
+    want = orc.prefill_attention(qp, kc16, vc16, bt, lens, cu, 0.1, dtype=orc.BF16)
+    np.testing.assert_array_equal(got, want)
