@@ -54,6 +54,10 @@ extern "C" {
 #define VPA_DTYPE_F32 0
 #define VPA_DTYPE_F16 1
 #define VPA_DTYPE_BF16 2
+/* OCP E4M3FN, cache element only (the reference's uint8 cache,
+ * vasr-paged-attn/src/metal/kernels/prefill_paged_attn.metal:698-722,
+ * 1610-1612): 1 byte, x = 16, dequantised as (float)byte * scale. */
+#define VPA_DTYPE_FP8_E4M3 3
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* vpa_last_error(void);
@@ -85,9 +89,12 @@ int vpa_cache_layout(int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
  *   key_cache  [blk, j, d / x, off, d % x] = key  [t, j, d]
  *   value_cache[blk, j, d, off]            = value[t, j, d]
  * Slots < 0 (PAD_SLOT_ID) and slots >= num_blocks*block_size are skipped.
- * The copy is bit-exact. k_scale / v_scale may be NULL; they are ignored
- * because cache_dtype must equal dtype (no fp8 cache in this build).
- * num_tokens == 0 is a no-op.
+ * With cache_dtype == dtype the copy is bit-exact and k_scale / v_scale may
+ * be NULL (ignored). With cache_dtype VPA_DTYPE_FP8_E4M3 (dtype f32, f16 or
+ * bf16) k_scale and v_scale are device pointers to one f32 each and every
+ * element is stored as E4M3FN(x / scale), rounded to nearest even and
+ * saturated to +-448 (NaN stays NaN) — the rule of the fp8 caches of the
+ * reference's paged-attention crate. num_tokens == 0 is a no-op.
  *
  * Cache strides: cache_block_stride / cache_head_stride are the element
  * strides of the first two dims of both caches (a (block, head) tile is
@@ -128,6 +135,10 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * at graph capture is fine as long as it is >= every context_len).
  * alibi_slopes and sinks must be NULL and softcapping must be 1.0 (the only
  * values vASR passes); anything else returns VPA_ERR_UNSUPPORTED.
+ * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 with a bf16 or f16
+ * query (head_dim 64 or 128, block_size 16 or 32): K and V are then read as
+ * (float)byte * (*k_scale) and (float)byte * (*v_scale), k_scale / v_scale
+ * being device pointers to one f32 each (ignored for 16/32-bit caches).
  * workspace must hold vpa_paged_attention_workspace_size(...) bytes (always
  * non-zero for num_seqs > 0: it carries the per-call work list) and be
  * 256-byte aligned. Two calls that run concurrently need two workspaces.
@@ -192,7 +203,10 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
  * out_key/out_value: [total_tokens, num_kv_heads, head_dim] packed in
  * out_dtype; row cu_seqlens_kv[s] + t holds token t of sequence s.
  * total_tokens must equal cu_seqlens_kv[num_seqs] (the host knows it from
- * kv_lens). Block ids >= num_blocks produce zero rows.
+ * kv_lens). Block ids >= num_blocks produce zero rows. out_dtype equals
+ * cache_dtype (bit-exact copy), or the cache is VPA_DTYPE_FP8_E4M3 and
+ * out_dtype f32 / f16 / bf16: each value is (float)byte * scale rounded to
+ * nearest even, with k_scale / v_scale device pointers to one f32 each.
  */
 int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
                         const void* value_cache, const float* k_scale, const float* v_scale,
@@ -227,7 +241,9 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
  * max_kv_len, which size the grid only; rows at or past total_query_rows are
  * neither read nor written. Block ids >= num_blocks are treated as absent.
  * out[row, h] = sum_t p_t V[t] / sum_t p_t (no epsilon, as flash attention).
- * Needs no workspace; safe under stream capture.
+ * cache_dtype must equal dtype (an fp8 cache returns VPA_ERR_UNSUPPORTED;
+ * gather it with vpa_gather_kv_cache first). Needs no workspace; safe under
+ * stream capture.
  */
 int vpa_chunked_prefill_paged_attention(
     void* out, const void* query, const float* k_scale, const float* v_scale,

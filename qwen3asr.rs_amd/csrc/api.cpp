@@ -40,6 +40,8 @@ int dtype_bytes(int32_t dtype) {
     case VPA_DTYPE_F16:
     case VPA_DTYPE_BF16:
       return 2;
+    case VPA_DTYPE_FP8_E4M3:
+      return 1;
     default:
       return 0;
   }
@@ -53,12 +55,30 @@ const char* dtype_name(int32_t dtype) {
       return "f16";
     case VPA_DTYPE_BF16:
       return "bf16";
+    case VPA_DTYPE_FP8_E4M3:
+      return "fp8_e4m3";
     default:
       return "unknown";
   }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool is_float_dtype(int32_t dtype) {
+  return dtype == VPA_DTYPE_F32 || dtype == VPA_DTYPE_F16 || dtype == VPA_DTYPE_BF16;
+}
+
+// An fp8 cache needs its two scales (device pointers to one f32 each).
+int check_scales(const char* op, int32_t cache_dtype, const float* k_scale,
+                 const float* v_scale) {
+  if (cache_dtype != VPA_DTYPE_FP8_E4M3) return VPA_OK;
+  if (k_scale == nullptr || v_scale == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: an fp8 cache needs k_scale and v_scale", op);
+  if ((reinterpret_cast<uintptr_t>(k_scale) & 3u) != 0 ||
+      (reinterpret_cast<uintptr_t>(v_scale) & 3u) != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: k_scale / v_scale must be 4-byte aligned", op);
+  return VPA_OK;
+}
 
 // Checks shared by every op that reads or writes the paged cache.
 int check_cache(const char* op, int32_t cache_dtype, int32_t num_kv_heads, int32_t head_dim,
@@ -175,16 +195,18 @@ int vpa_reshape_and_cache(const void* key, const void* value, int64_t key_token_
                           int64_t num_blocks, int64_t cache_block_stride,
                           int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
                           void* stream) {
-  (void)k_scale;
-  (void)v_scale;
   clear_error();
   const char* op = "reshape_and_cache";
   if (num_tokens < 0) return fail(VPA_ERR_INVALID_ARGUMENT, "%s: num_tokens < 0", op);
-  if (dtype != cache_dtype)
+  if (!is_float_dtype(dtype))
+    return fail(VPA_ERR_UNSUPPORTED, "%s: unsupported input dtype %s", op, dtype_name(dtype));
+  if (dtype != cache_dtype && cache_dtype != VPA_DTYPE_FP8_E4M3)
     return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from input dtype %s", op,
                 dtype_name(cache_dtype), dtype_name(dtype));
   int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
                        cache_block_stride, cache_head_stride, key_cache, value_cache);
+  if (rc != VPA_OK) return rc;
+  rc = check_scales(op, cache_dtype, k_scale, v_scale);
   if (rc != VPA_OK) return rc;
   if (num_tokens == 0) return VPA_OK;
   if (key == nullptr || value == nullptr || slot_mapping == nullptr)
@@ -202,9 +224,10 @@ int vpa_reshape_and_cache(const void* key, const void* value, int64_t key_token_
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: too many tokens: %lld", op, (long long)num_tokens);
   CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
               cache_head_stride};
-  return hip_status(op, launch_reshape_and_cache(dtype, key, value, key_token_stride,
-                                                 value_token_stride, key_cache, value_cache,
-                                                 slot_mapping, num_tokens, g,
+  return hip_status(op, launch_reshape_and_cache(dtype, cache_dtype, key, value,
+                                                 key_token_stride, value_token_stride,
+                                                 key_cache, value_cache, slot_mapping,
+                                                 num_tokens, g, k_scale, v_scale,
                                                  static_cast<hipStream_t>(stream)));
 }
 
@@ -218,7 +241,8 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
 namespace {
 
 // paged_attention and its planned variant: all checks, then the launch.
-int paged_attention_impl(void* out, const void* query, const void* key_cache,
+int paged_attention_impl(void* out, const void* query, const float* k_scale,
+                         const float* v_scale, const void* key_cache,
                          const void* value_cache, const uint32_t* block_tables,
                          int32_t block_table_stride, const uint32_t* context_lens,
                          const float* alibi_slopes, int32_t max_context_len, float softmax_scale,
@@ -235,12 +259,20 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache,
   if (softcapping != 1.0f)
     return fail(VPA_ERR_UNSUPPORTED, "%s: softcapping must be 1.0 (off), got %g", op,
                 (double)softcapping);
-  if (dtype != cache_dtype)
+  const bool fp8 = cache_dtype == VPA_DTYPE_FP8_E4M3;
+  if (dtype != cache_dtype &&
+      !(fp8 && (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16)))
     return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from query dtype %s", op,
                 dtype_name(cache_dtype), dtype_name(dtype));
   int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
                        cache_block_stride, cache_head_stride, key_cache, value_cache);
   if (rc != VPA_OK) return rc;
+  rc = check_scales(op, cache_dtype, k_scale, v_scale);
+  if (rc != VPA_OK) return rc;
+  if (fp8 && !((head_dim == 64 || head_dim == 128) && (block_size == 16 || block_size == 32)))
+    return fail(VPA_ERR_UNSUPPORTED,
+                "%s: fp8 cache needs head_dim 64 or 128 and block_size 16 or 32 (got %d, %d)", op,
+                head_dim, block_size);
   if (num_seqs < 0 || num_heads <= 0 || max_context_len < 0 || block_table_stride < 0)
     return fail(VPA_ERR_INVALID_ARGUMENT,
                 "%s: bad sizes num_seqs=%d num_heads=%d max_context_len=%d "
@@ -292,10 +324,11 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache,
   DecodeWorkspace ws =
       carve_decode_workspace(workspace, num_seqs, num_heads, head_dim, max_context_len);
   ws.planned = planned;
-  return hip_status(op, launch_paged_decode(dtype, out, query, key_cache, value_cache,
-                                            block_tables, block_table_stride, context_lens,
-                                            max_context_len, softmax_scale, num_seqs, num_heads,
-                                            g, ws, static_cast<hipStream_t>(stream)));
+  return hip_status(op, launch_paged_decode(dtype, cache_dtype, out, query, key_cache,
+                                            value_cache, block_tables, block_table_stride,
+                                            context_lens, max_context_len, softmax_scale,
+                                            k_scale, v_scale, num_seqs, num_heads, g, ws,
+                                            static_cast<hipStream_t>(stream)));
 }
 
 }  // namespace
@@ -312,10 +345,8 @@ int vpa_paged_attention(void* out, const void* query, const float* k_scale,
                         int64_t num_blocks, int64_t cache_block_stride,
                         int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
                         void* workspace, size_t workspace_bytes, void* stream) {
-  (void)k_scale;
-  (void)v_scale;
-  return paged_attention_impl(out, query, key_cache, value_cache, block_tables,
-                              block_table_stride, context_lens, alibi_slopes, max_context_len,
+  return paged_attention_impl(out, query, k_scale, v_scale, key_cache, value_cache,
+                              block_tables, block_table_stride, context_lens, alibi_slopes, max_context_len,
                               softmax_scale, softcapping, sinks, num_seqs, num_heads,
                               num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
                               cache_head_stride, dtype, cache_dtype, workspace, workspace_bytes,
@@ -333,10 +364,8 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
                                 int64_t cache_block_stride, int64_t cache_head_stride,
                                 int32_t dtype, int32_t cache_dtype, void* workspace,
                                 size_t workspace_bytes, void* stream) {
-  (void)k_scale;
-  (void)v_scale;
-  return paged_attention_impl(out, query, key_cache, value_cache, block_tables,
-                              block_table_stride, context_lens, alibi_slopes, max_context_len,
+  return paged_attention_impl(out, query, k_scale, v_scale, key_cache, value_cache,
+                              block_tables, block_table_stride, context_lens, alibi_slopes, max_context_len,
                               softmax_scale, softcapping, sinks, num_seqs, num_heads,
                               num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
                               cache_head_stride, dtype, cache_dtype, workspace, workspace_bytes,
@@ -393,15 +422,16 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
                         int64_t num_blocks, int64_t cache_block_stride,
                         int64_t cache_head_stride, int32_t cache_dtype, int32_t out_dtype,
                         void* stream) {
-  (void)k_scale;
-  (void)v_scale;
   clear_error();
   const char* op = "gather_kv_cache";
-  if (out_dtype != cache_dtype)
+  if (out_dtype != cache_dtype &&
+      !(cache_dtype == VPA_DTYPE_FP8_E4M3 && is_float_dtype(out_dtype)))
     return fail(VPA_ERR_UNSUPPORTED, "%s: out dtype %s differs from cache dtype %s", op,
                 dtype_name(out_dtype), dtype_name(cache_dtype));
   int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
                        cache_block_stride, cache_head_stride, key_cache, value_cache);
+  if (rc != VPA_OK) return rc;
+  rc = check_scales(op, cache_dtype, k_scale, v_scale);
   if (rc != VPA_OK) return rc;
   if (num_seqs < 0 || total_tokens < 0 || block_table_stride < 0)
     return fail(VPA_ERR_INVALID_ARGUMENT,
@@ -418,9 +448,10 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: outputs must be 16-byte aligned", op);
   CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
               cache_head_stride};
-  return hip_status(op, launch_gather_kv_cache(cache_dtype, out_key, out_value, key_cache,
-                                               value_cache, block_tables, block_table_stride,
-                                               cu_seqlens_kv, num_seqs, g,
+  return hip_status(op, launch_gather_kv_cache(cache_dtype, out_dtype, out_key, out_value,
+                                               key_cache, value_cache, block_tables,
+                                               block_table_stride, cu_seqlens_kv, num_seqs, g,
+                                               k_scale, v_scale,
                                                static_cast<hipStream_t>(stream)));
 }
 

@@ -39,8 +39,11 @@ __device__ __forceinline__ void store_stream(uint4* dst, const uint4& v) {
 }
 template <typename T>
 __device__ __forceinline__ void store_stream(T* dst, T v) {
-  static_assert(sizeof(T) == 2 || sizeof(T) == 4, "cache element");
-  if constexpr (sizeof(T) == 2)
+  static_assert(sizeof(T) == 1 || sizeof(T) == 2 || sizeof(T) == 4, "cache element");
+  if constexpr (sizeof(T) == 1)
+    __builtin_nontemporal_store(__builtin_bit_cast(unsigned char, v),
+                                reinterpret_cast<unsigned char*>(dst));
+  else if constexpr (sizeof(T) == 2)
     __builtin_nontemporal_store(__builtin_bit_cast(unsigned short, v),
                                 reinterpret_cast<unsigned short*>(dst));
   else
@@ -48,13 +51,33 @@ __device__ __forceinline__ void store_stream(T* dst, T v) {
                                 reinterpret_cast<unsigned int*>(dst));
 }
 
-template <typename T, int D, int BS>
+// Sixteen consecutive elements of T, each divided by `scale` and encoded as
+// E4M3FN, packed into one 16-byte vector (byte e = element e).
+template <typename T>
+__device__ __forceinline__ uint4 quantize16(const T* src, float scale) {
+  uint32_t w[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t b = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) b |= fp8_from_f32(load_as_f32(src + 4 * q + e) / scale) << (8 * e);
+    w[q] = b;
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// T: element type of the new rows; C: cache element type (T itself, copied
+// bit-exactly, or fp8_t, quantised with *k_scale / *v_scale).
+template <typename T, typename C, int D, int BS>
 __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
     const T* __restrict__ key, const T* __restrict__ value, int64_t key_token_stride,
-    int64_t value_token_stride, T* __restrict__ key_cache, T* __restrict__ value_cache,
+    int64_t value_token_stride, C* __restrict__ key_cache, C* __restrict__ value_cache,
     const int64_t* __restrict__ slot_mapping, int64_t num_tokens, int64_t num_slots,
-    int64_t block_stride, int64_t head_stride) {
-  constexpr int X = pack_x<T>();
+    int64_t block_stride, int64_t head_stride, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale) {
+  constexpr bool kQuant = !std::is_same_v<T, C>;
+  static_assert(!kQuant || std::is_same_v<C, fp8_t>, "a cache type differing from the rows is fp8");
+  constexpr int X = pack_x<C>();
   constexpr int CH = D / X;       // 16-byte chunks per row
   constexpr int NV = CH * BS;     // 16-byte vectors per tile
   constexpr int VR = BS / X;      // 16-byte vectors per value-tile row (may be 0)
@@ -74,15 +97,25 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
     if (s >= num_slots) s = -1;  // out-of-range slots are skipped like padding
     slots[tid] = s;
   }
+  float ks = 1.f, vs = 1.f;
+  if constexpr (kQuant) {
+    ks = *k_scale;
+    vs = *v_scale;
+  }
   for (int i = tid; i < NV; i += kThreads) {
     const int t = i / CH;
     const int c = i - t * CH;
     const int64_t tok = t0 + t;
     if (tok < num_tokens) {
-      k_rows[i] = *reinterpret_cast<const uint4*>(key + tok * key_token_stride +
-                                                  (int64_t)head * D + c * X);
-      v_rows[i] = *reinterpret_cast<const uint4*>(value + tok * value_token_stride +
-                                                  (int64_t)head * D + c * X);
+      const T* ksrc = key + tok * key_token_stride + (int64_t)head * D + c * X;
+      const T* vsrc = value + tok * value_token_stride + (int64_t)head * D + c * X;
+      if constexpr (kQuant) {
+        k_rows[i] = quantize16(ksrc, ks);
+        v_rows[i] = quantize16(vsrc, vs);
+      } else {
+        k_rows[i] = *reinterpret_cast<const uint4*>(ksrc);
+        v_rows[i] = *reinterpret_cast<const uint4*>(vsrc);
+      }
     }
   }
   __syncthreads();
@@ -96,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
     const int64_t blk = s0 / BS;
     uint4* kt = reinterpret_cast<uint4*>(key_cache + blk * block_stride + head * head_stride);
     uint4* vt = reinterpret_cast<uint4*>(value_cache + blk * block_stride + head * head_stride);
-    const T* vsrc = reinterpret_cast<const T*>(v_rows);
+    const C* vsrc = reinterpret_cast<const C*>(v_rows);
     for (int i = tid; i < NV; i += kThreads) {
       // key tile vector i = (chunk c, offset t)
       const int c = i / BS;
@@ -107,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
       const int sg = i - d * (VR > 0 ? VR : 1);
       union {
         uint4 v;
-        T e[X];
+        C e[X];
       } u;
 #pragma unroll
       for (int e = 0; e < X; ++e) u.e[e] = vsrc[(sg * X + e) * D + d];
@@ -137,7 +170,7 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
         else *dst = k_rows[t * CH + c];
       }
     }
-    const T* vsrc = reinterpret_cast<const T*>(v_rows);
+    const C* vsrc = reinterpret_cast<const C*>(v_rows);
     for (int i = tid; i < D * BS; i += kThreads) {
       const int d = i / BS;
       const int t = i - d * BS;
@@ -145,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
       if (s >= 0) {
         const int64_t blk = s / BS;
         const int off = (int)(s - blk * BS);
-        T* dst = &value_cache[blk * block_stride + head * head_stride + (int64_t)d * BS + off];
+        C* dst = &value_cache[blk * block_stride + head * head_stride + (int64_t)d * BS + off];
         if constexpr (decltype(streaming)::value) store_stream(dst, vsrc[t * D + d]);
         else *dst = vsrc[t * D + d];
       }
@@ -227,17 +260,165 @@ __global__ __launch_bounds__(kThreads) void gather_kv_cache_kernel(
   }
 }
 
+// Sixteen f32 values stored as TO (round to nearest even) with 16-byte stores.
+template <typename TO>
+__device__ __forceinline__ void store16(TO* dst, const float (&f)[16]) {
+  uint4* d4 = reinterpret_cast<uint4*>(dst);
+  if constexpr (std::is_same_v<TO, float>) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      d4[q] = make_uint4(__float_as_uint(f[4 * q]), __float_as_uint(f[4 * q + 1]),
+                         __float_as_uint(f[4 * q + 2]), __float_as_uint(f[4 * q + 3]));
+  } else {
+    uint32_t w[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      TO lo, hi;
+      store_from_f32<TO>(&lo, f[2 * q]);
+      store_from_f32<TO>(&hi, f[2 * q + 1]);
+      w[q] = (uint32_t)lo.x | ((uint32_t)hi.x << 16);
+    }
+    d4[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    d4[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  }
+}
+
+// Sixteen E4M3FN bytes -> f32 times `scale`, through the same exact
+// conversion the decode kernel uses (to f16 for an f16 output, to bf16
+// otherwise), then widened. The sign of each result is set last from the
+// byte and the scale: the f16 path and a fused multiply-add with a +0
+// addend (v_fma_mix, which the compiler picks for f16 -> f32 * s -> f16)
+// both turn -0 into +0; every other value already has that sign.
+template <typename TO>
+__device__ __forceinline__ void fp8x16_to_f32_scaled(const uint4& v, float scale,
+                                                     float (&f)[16]) {
+  using P = std::conditional_t<std::is_same_v<TO, f16_t>, f16_t, bf16_t>;
+  uint4 lo, hi;
+  fp8x16_to_pk<P>(v, lo, hi);
+  const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  const uint32_t b[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    if constexpr (std::is_same_v<P, f16_t>) {
+      f[2 * q] = f16_bits_to_f32((uint16_t)(w[q] & 0xffffu));
+      f[2 * q + 1] = f16_bits_to_f32((uint16_t)(w[q] >> 16));
+    } else {
+      f[2 * q] = bf16_bits_to_f32(w[q] & 0xffffu);
+      f[2 * q + 1] = bf16_bits_to_f32(w[q] >> 16);
+    }
+  }
+  const uint32_t sneg = __float_as_uint(scale) >> 31;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const uint32_t neg = ((b[e / 4] >> (8 * (e % 4) + 7)) & 1u) ^ sneg;
+    const float m = f[e] * scale;
+    f[e] = __uint_as_float((__float_as_uint(m) & 0x7fffffffu) | (neg << 31));
+  }
+}
+
+// gather_kv_cache from an fp8 cache: like gather_kv_cache_kernel, each value
+// dequantised as (float)byte * scale and stored as TO.
+template <typename TO, int D, int BS>
+__global__ __launch_bounds__(kThreads) void gather_kv_cache_fp8_kernel(
+    TO* __restrict__ out_key, TO* __restrict__ out_value, const fp8_t* __restrict__ key_cache,
+    const fp8_t* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
+    int32_t block_table_stride, const uint32_t* __restrict__ cu_seqlens, int64_t num_blocks,
+    int64_t block_stride, int64_t head_stride, int32_t num_kv_heads,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
+  constexpr int X = 16;
+  constexpr int CH = D / X;
+  constexpr int NV = CH * BS;  // 16-byte vectors per tile (K and V alike)
+
+  __shared__ uint4 k_tile[NV];
+  __shared__ __align__(16) uint8_t v_tile[D * BS];
+
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int s = blockIdx.y;
+  const int head = blockIdx.z;
+  const uint32_t row0 = cu_seqlens[s];
+  const int64_t kv_len = (int64_t)cu_seqlens[s + 1] - (int64_t)row0;
+  const int64_t tok0 = (int64_t)b * BS;
+  if (tok0 >= kv_len) return;
+  const int ntok = (int)min((int64_t)BS, kv_len - tok0);
+  const uint32_t phys = block_tables[(int64_t)s * block_table_stride + b];
+  const bool valid = (int64_t)phys < num_blocks;
+
+  if (valid) {
+    const int64_t off = (int64_t)phys * block_stride + head * head_stride;
+    const uint4* kt = reinterpret_cast<const uint4*>(key_cache + off);
+    const uint4* vt = reinterpret_cast<const uint4*>(value_cache + off);
+    uint4* vdst = reinterpret_cast<uint4*>(v_tile);
+    for (int i = tid; i < NV; i += kThreads) {
+      k_tile[i] = kt[i];
+      vdst[i] = vt[i];
+    }
+  }
+  __syncthreads();
+  const float ks = *k_scale, vs = *v_scale;
+  const int64_t row_stride = (int64_t)num_kv_heads * D;
+  for (int i = tid; i < NV; i += kThreads) {
+    const int t = i / CH;
+    const int c = i - t * CH;
+    if (t >= ntok) continue;
+    const int64_t o = ((int64_t)row0 + tok0 + t) * row_stride + (int64_t)head * D + c * X;
+    float f[16];
+    if (valid) {
+      fp8x16_to_f32_scaled<TO>(k_tile[c * BS + t], ks, f);  // key tile vector (c, t)
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) f[e] = 0.f;
+    }
+    store16(out_key + o, f);
+    if (valid) {
+      uint32_t w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t bword = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bword |= (uint32_t)v_tile[(c * X + 4 * q + e) * BS + t] << (8 * e);
+        w[q] = bword;
+      }
+      fp8x16_to_f32_scaled<TO>(make_uint4(w[0], w[1], w[2], w[3]), vs, f);
+    }
+    store16(out_value + o, f);
+  }
+}
+
+template <typename TO, int D, int BS>
+hipError_t launch_gather_fp8(void* ok, void* ov, const void* kc, const void* vc,
+                             const uint32_t* bt, int32_t bts, const uint32_t* cu,
+                             int32_t num_seqs, const CacheGeom& g, const float* k_scale,
+                             const float* v_scale, hipStream_t stream) {
+  dim3 grid((unsigned)bts, (unsigned)num_seqs, (unsigned)g.num_kv_heads);
+  hipLaunchKernelGGL((gather_kv_cache_fp8_kernel<TO, D, BS>), grid, dim3(kThreads), 0, stream,
+                     static_cast<TO*>(ok), static_cast<TO*>(ov), static_cast<const fp8_t*>(kc),
+                     static_cast<const fp8_t*>(vc), bt, bts, cu, g.num_blocks, g.block_stride,
+                     g.head_stride, g.num_kv_heads, k_scale, v_scale);
+  return hipGetLastError();
+}
+
+template <typename T, typename C, int D, int BS>
+hipError_t launch_rc_t(const void* key, const void* value, int64_t kts, int64_t vts, void* kc,
+                       void* vc, const int64_t* slots, int64_t num_tokens, const CacheGeom& g,
+                       const float* k_scale, const float* v_scale, hipStream_t stream) {
+  const int64_t groups = (num_tokens + BS - 1) / BS;
+  dim3 grid((unsigned)groups, (unsigned)g.num_kv_heads);
+  hipLaunchKernelGGL((reshape_and_cache_kernel<T, C, D, BS>), grid, dim3(kThreads), 0, stream,
+                     static_cast<const T*>(key), static_cast<const T*>(value), kts, vts,
+                     static_cast<C*>(kc), static_cast<C*>(vc), slots, num_tokens,
+                     g.num_blocks * (int64_t)BS, g.block_stride, g.head_stride, k_scale, v_scale);
+  return hipGetLastError();
+}
 template <typename T, int D, int BS>
 hipError_t launch_rc(const void* key, const void* value, int64_t kts, int64_t vts, void* kc,
                      void* vc, const int64_t* slots, int64_t num_tokens, const CacheGeom& g,
-                     hipStream_t stream) {
-  const int64_t groups = (num_tokens + BS - 1) / BS;
-  dim3 grid((unsigned)groups, (unsigned)g.num_kv_heads);
-  hipLaunchKernelGGL((reshape_and_cache_kernel<T, D, BS>), grid, dim3(kThreads), 0, stream,
-                     static_cast<const T*>(key), static_cast<const T*>(value), kts, vts,
-                     static_cast<T*>(kc), static_cast<T*>(vc), slots, num_tokens,
-                     g.num_blocks * (int64_t)BS, g.block_stride, g.head_stride);
-  return hipGetLastError();
+                     const float* k_scale, const float* v_scale, bool fp8, hipStream_t stream) {
+  if (fp8)
+    return launch_rc_t<T, fp8_t, D, BS>(key, value, kts, vts, kc, vc, slots, num_tokens, g,
+                                        k_scale, v_scale, stream);
+  return launch_rc_t<T, T, D, BS>(key, value, kts, vts, kc, vc, slots, num_tokens, g, k_scale,
+                                  v_scale, stream);
 }
 
 template <typename T, int D, int BS>
@@ -276,7 +457,16 @@ hipError_t dispatch_rc(int dtype, int D, int BS, A... args) {
 }
 
 template <typename... A>
+hipError_t dispatch_gather_fp8(int out_dtype, int D, int BS, A... args) {
+  if (out_dtype == VPA_DTYPE_F32) { VPA_CACHE_CASES(launch_gather_fp8, float) }
+  if (out_dtype == VPA_DTYPE_BF16) { VPA_CACHE_CASES(launch_gather_fp8, bf16_t) }
+  if (out_dtype == VPA_DTYPE_F16) { VPA_CACHE_CASES(launch_gather_fp8, f16_t) }
+  return hipErrorInvalidValue;
+}
+
+template <typename... A>
 hipError_t dispatch_gather(int dtype, int D, int BS, A... args) {
+  if (dtype == VPA_DTYPE_FP8_E4M3) { VPA_CACHE_CASES(launch_gather, fp8_t) }  // raw bytes
   if (dtype == VPA_DTYPE_F32) { VPA_CACHE_CASES(launch_gather, float) }
   if (dtype == VPA_DTYPE_BF16) { VPA_CACHE_CASES(launch_gather, bf16_t) }
   if (dtype == VPA_DTYPE_F16) { VPA_CACHE_CASES(launch_gather, f16_t) }
@@ -286,28 +476,35 @@ hipError_t dispatch_gather(int dtype, int D, int BS, A... args) {
 }  // namespace
 
 bool cache_kernels_supported(int dtype, int head_dim, int block_size) {
-  const bool dt = dtype == VPA_DTYPE_F32 || dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16;
+  const bool dt = dtype == VPA_DTYPE_F32 || dtype == VPA_DTYPE_BF16 ||
+                  dtype == VPA_DTYPE_F16 || dtype == VPA_DTYPE_FP8_E4M3;
   const bool d = head_dim == 64 || head_dim == 128 || head_dim == 256;
   const bool bs = block_size == 8 || block_size == 16 || block_size == 32;
   return dt && d && bs;
 }
 
-hipError_t launch_reshape_and_cache(int dtype, const void* key, const void* value,
-                                    int64_t key_token_stride, int64_t value_token_stride,
-                                    void* key_cache, void* value_cache,
-                                    const int64_t* slot_mapping, int64_t num_tokens,
-                                    const CacheGeom& g, hipStream_t stream) {
+hipError_t launch_reshape_and_cache(int dtype, int cache_dtype, const void* key,
+                                    const void* value, int64_t key_token_stride,
+                                    int64_t value_token_stride, void* key_cache,
+                                    void* value_cache, const int64_t* slot_mapping,
+                                    int64_t num_tokens, const CacheGeom& g, const float* k_scale,
+                                    const float* v_scale, hipStream_t stream) {
   return dispatch_rc(dtype, g.head_dim, g.block_size, key, value, key_token_stride,
                      value_token_stride, key_cache, value_cache, slot_mapping, num_tokens, g,
-                     stream);
+                     k_scale, v_scale, cache_dtype == VPA_DTYPE_FP8_E4M3, stream);
 }
 
-hipError_t launch_gather_kv_cache(int dtype, void* out_key, void* out_value,
-                                  const void* key_cache, const void* value_cache,
-                                  const uint32_t* block_tables, int32_t block_table_stride,
-                                  const uint32_t* cu_seqlens, int32_t num_seqs,
-                                  const CacheGeom& g, hipStream_t stream) {
-  return dispatch_gather(dtype, g.head_dim, g.block_size, out_key, out_value, key_cache,
+hipError_t launch_gather_kv_cache(int cache_dtype, int out_dtype, void* out_key,
+                                  void* out_value, const void* key_cache,
+                                  const void* value_cache, const uint32_t* block_tables,
+                                  int32_t block_table_stride, const uint32_t* cu_seqlens,
+                                  int32_t num_seqs, const CacheGeom& g, const float* k_scale,
+                                  const float* v_scale, hipStream_t stream) {
+  if (cache_dtype == VPA_DTYPE_FP8_E4M3)
+    return dispatch_gather_fp8(out_dtype, g.head_dim, g.block_size, out_key, out_value,
+                               key_cache, value_cache, block_tables, block_table_stride,
+                               cu_seqlens, num_seqs, g, k_scale, v_scale, stream);
+  return dispatch_gather(cache_dtype, g.head_dim, g.block_size, out_key, out_value, key_cache,
                          value_cache, block_tables, block_table_stride, cu_seqlens, num_seqs,
                          g, stream);
 }

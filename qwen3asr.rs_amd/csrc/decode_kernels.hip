@@ -26,6 +26,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "vpa_device.h"
 #include "vpa_internal.h"
@@ -352,17 +353,37 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(
 // work unit. Wave w attends over partition w of the chunk (PT tokens); the NW
 // partial results are merged in LDS, so HBM partial rows are only written for
 // sequences longer than one chunk.
-template <typename T, int D, int BS, int G, int PT, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(VPA_DECODE_ROWS_WAVES_PER_EU)))
+//
+// C is the cache element type: T itself, or fp8_t (E4M3FN bytes, 16 per
+// vector). With fp8 each 16-byte K or V vector is converted once to two
+// vectors of T (exact, v_cvt_scalef32_pk_*_fp8 with scale 1) and the same
+// v_dot2 products follow; a lane's q chunk is then 16 dims (two vectors),
+// *k_scale is folded into the softmax scale and *v_scale into the output.
+// Waves per SIMD the rows kernel is compiled for: instances with many q
+// vectors per lane (16-byte vectors: G x chunks per lane, two per chunk for
+// fp8) would spill at 3 (measured: fp8 at 16, 16-bit at 32).
+template <typename C, int D, int BS, int G>
+constexpr int rows_waves_per_eu() {
+  constexpr bool f8 = sizeof(C) == 1;
+  constexpr int qvec = G * (D * BS / ((f8 ? 16 : 8) * 64)) * (f8 ? 2 : 1);
+  return (f8 ? qvec >= 16 : qvec > 16) ? 2 : VPA_DECODE_ROWS_WAVES_PER_EU;
+}
+
+template <typename T, typename C, int D, int BS, int G, int PT, int NW>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(rows_waves_per_eu<C, D, BS, G>())))
 void paged_decode_rows_kernel(
-    T* __restrict__ out, const T* __restrict__ query, const T* __restrict__ key_cache,
-    const T* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
+    T* __restrict__ out, const T* __restrict__ query, const C* __restrict__ key_cache,
+    const C* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
     int32_t block_table_stride, float scale, int32_t num_heads, int32_t num_kv_heads,
     int64_t num_blocks, int64_t block_stride, int64_t head_stride, float* __restrict__ part_out,
     int32_t max_parts, const uint2* __restrict__ items, const uint32_t* __restrict__ queue,
-    int32_t num_seqs, int32_t max_ctx, int32_t cap_tokens) {
-  constexpr int X = pack_x<T>();
-  static_assert(X == 8, "16-bit element types only");
+    int32_t num_seqs, int32_t max_ctx, int32_t cap_tokens, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale) {
+  constexpr bool kF8 = std::is_same_v<C, fp8_t>;
+  static_assert(kF8 || std::is_same_v<C, T>, "cache type is the query type or fp8");
+  constexpr int X = pack_x<C>();
+  static_assert(X == (kF8 ? 16 : 8), "16-bit or fp8 cache elements only");
   constexpr int PB = PT / BS;        // blocks per wave partition
   constexpr int VPR = BS / X;        // 16-byte vectors per value row
   constexpr int NVV = D * VPR / 64;  // value vectors per lane per block
@@ -424,17 +445,27 @@ void paged_decode_rows_kernel(
     for (int k = 0; k < NVV; ++k) acc[g][k] = 0.f;
   }
 
+  float vs = 1.f;  // value scale of an fp8 cache
+  if constexpr (kF8) {
+    scale *= *k_scale;
+    vs = *v_scale;
+  }
+
   if (nb > 0) {
     // block ids of the partition (lane b holds block b) and this lane's q chunks
     const uint32_t my_bt =
         lane < nb ? block_tables[(int64_t)s * block_table_stride + b_begin + lane] : 0u;
-    uint4 qv[G][KPL];
+    constexpr int QV = kF8 ? 2 : 1;  // 16-byte vectors of q per chunk
+    uint4 qv[G][KPL][QV];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const T* qrow = query + ((int64_t)s * num_heads + j * G + g) * D;
 #pragma unroll
       for (int k = 0; k < KPL; ++k)
-        qv[g][k] = *reinterpret_cast<const uint4*>(qrow + (lane / BS + k * LPT) * X);
+#pragma unroll
+        for (int h2 = 0; h2 < QV; ++h2)
+          qv[g][k][h2] =
+              *reinterpret_cast<const uint4*>(qrow + (lane / BS + k * LPT) * X + 8 * h2);
     }
 
     const int64_t head_off = (int64_t)j * head_stride;
@@ -473,13 +504,26 @@ void paged_decode_rows_kernel(
         tile_block(st, u, ok);
         const int bi = st * BKS + u;
         const bool valid = ok && (b_begin + bi) * BS + t < L;
+        float qk[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) qk[g] = 0.f;
+#pragma unroll
+        for (int k = 0; k < KPL; ++k) {
+          if constexpr (kF8) {
+            uint4 klo, khi;
+            fp8x16_to_pk<T>(buf[u * KPL + k], klo, khi);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+              qk[g] = dot16<T>(qv[g][k][1], khi, dot16<T>(qv[g][k][0], klo, qk[g]));
+          } else {
+#pragma unroll
+            for (int g = 0; g < G; ++g) qk[g] = dot16<T>(qv[g][k][0], buf[u * KPL + k], qk[g]);
+          }
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          float qk = 0.f;
-#pragma unroll
-          for (int k = 0; k < KPL; ++k) qk = dot16<T>(qv[g][k], buf[u * KPL + k], qk);
-          qk = sum_lanes_mod<BS>(qk);
-          if (lane < BS && bi < PB) my_logit[g * PT + bi * BS + lane] = valid ? qk * scale : -INFINITY;
+          const float r = sum_lanes_mod<BS>(qk[g]);
+          if (lane < BS && bi < PB) my_logit[g * PT + bi * BS + lane] = valid ? r * scale : -INFINITY;
         }
       }
     };
@@ -495,13 +539,40 @@ void paged_decode_rows_kernel(
 #pragma unroll
         for (int k = 0; k < NVV; ++k) vv[k] = buf[u * KPL + k];
         const int tok0 = (b_begin + bi) * BS + seg * X;
+        if constexpr (kF8) {
+#pragma unroll
+          for (int k = 0; k < NVV; ++k) {
+            uint4 vh[2];
+            fp8x16_to_pk<T>(vv[k], vh[0], vh[1]);
+            if (tok0 + X > L) {  // past the context in the last block: stale values
+#pragma unroll
+              for (int h2 = 0; h2 < 2; ++h2) {
+                union {
+                  uint4 v;
+                  uint16_t e[8];
+                } wv;
+                wv.v = vh[h2];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  if (tok0 + 8 * h2 + e >= L) wv.e[e] = 0;
+                vh[h2] = wv.v;
+              }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const uint4* pp = reinterpret_cast<const uint4*>(&my_p[g * PT + bi * BS + seg * X]);
+              acc[g][k] = dot16<T>(pp[1], vh[1], dot16<T>(pp[0], vh[0], acc[g][k]));
+            }
+          }
+          continue;
+        }
         if (tok0 + X > L) {
           // past the context in the last block: zero the values (stale contents)
 #pragma unroll
           for (int k = 0; k < NVV; ++k) {
             union {
               uint4 v;
-              uint16_t e[X];
+              uint16_t e[8];
             } wv;
             wv.v = vv[k];
 #pragma unroll
@@ -582,6 +653,7 @@ void paged_decode_rows_kernel(
       for (int k = 0; k < NVV; ++k) {
         if constexpr (VPR >= 2) acc[g][k] += dpp<kDppQuadXor1>(acc[g][k]);
         if constexpr (VPR >= 4) acc[g][k] += dpp<kDppQuadXor2>(acc[g][k]);
+        if constexpr (kF8) acc[g][k] *= vs;
       }
   }
 
@@ -747,11 +819,12 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   }
 }
 
-template <typename T, int D, int BS, int G>
-hipError_t launch_decode_rows(void* out, const void* q, const void* kc, const void* vc,
-                              const uint32_t* bt, int32_t bts, const uint32_t* cl,
-                              int32_t max_ctx, float scale, int32_t num_seqs, int32_t num_heads,
-                              const CacheGeom& g, const DecodeWorkspace& ws, hipStream_t stream) {
+template <typename T, typename C, int D, int BS, int G>
+hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const void* vc,
+                                const uint32_t* bt, int32_t bts, const uint32_t* cl,
+                                int32_t max_ctx, float scale, int32_t num_seqs,
+                                int32_t num_heads, const CacheGeom& g, const DecodeWorkspace& ws,
+                                hipStream_t stream, const float* k_scale, const float* v_scale) {
   constexpr int kChunk = kRowsPT * kRowsWaves;  // tokens per workgroup
   const int cap_tokens = bts * g.block_size;
   hipError_t e = hipSuccess;
@@ -763,12 +836,12 @@ hipError_t launch_decode_rows(void* out, const void* q, const void* kc, const vo
   }
   const int max_chunks = max(1, (max_ctx + kChunk - 1) / kChunk);
   const int64_t units = (int64_t)num_seqs * max_chunks * g.num_kv_heads;
-  hipLaunchKernelGGL((paged_decode_rows_kernel<T, D, BS, G, kRowsPT, kRowsWaves>),
+  hipLaunchKernelGGL((paged_decode_rows_kernel<T, C, D, BS, G, kRowsPT, kRowsWaves>),
                      dim3((unsigned)units), dim3(64 * kRowsWaves), 0, stream,
-                     static_cast<T*>(out), static_cast<const T*>(q), static_cast<const T*>(kc),
-                     static_cast<const T*>(vc), bt, bts, scale, num_heads, g.num_kv_heads,
+                     static_cast<T*>(out), static_cast<const T*>(q), static_cast<const C*>(kc),
+                     static_cast<const C*>(vc), bt, bts, scale, num_heads, g.num_kv_heads,
                      g.num_blocks, g.block_stride, g.head_stride, ws.part_out, ws.max_parts,
-                     ws.items, ws.queue, num_seqs, max_ctx, cap_tokens);
+                     ws.items, ws.queue, num_seqs, max_ctx, cap_tokens, k_scale, v_scale);
   e = hipGetLastError();
   if (e != hipSuccess || max_chunks <= 1) return e;
   const int64_t munits = (int64_t)num_seqs * num_heads;
@@ -780,10 +853,33 @@ hipError_t launch_decode_rows(void* out, const void* q, const void* kc, const vo
 }
 
 template <typename T, int D, int BS, int G>
+hipError_t launch_decode_rows(void* out, const void* q, const void* kc, const void* vc,
+                              const uint32_t* bt, int32_t bts, const uint32_t* cl,
+                              int32_t max_ctx, float scale, int32_t num_seqs, int32_t num_heads,
+                              const CacheGeom& g, const DecodeWorkspace& ws, hipStream_t stream,
+                              const float* k_scale, const float* v_scale) {
+  return launch_decode_rows_c<T, T, D, BS, G>(out, q, kc, vc, bt, bts, cl, max_ctx, scale,
+                                              num_seqs, num_heads, g, ws, stream, k_scale,
+                                              v_scale);
+}
+template <typename T, int D, int BS, int G>
+hipError_t launch_decode_rows_fp8(void* out, const void* q, const void* kc, const void* vc,
+                                  const uint32_t* bt, int32_t bts, const uint32_t* cl,
+                                  int32_t max_ctx, float scale, int32_t num_seqs,
+                                  int32_t num_heads, const CacheGeom& g,
+                                  const DecodeWorkspace& ws, hipStream_t stream,
+                                  const float* k_scale, const float* v_scale) {
+  return launch_decode_rows_c<T, fp8_t, D, BS, G>(out, q, kc, vc, bt, bts, cl, max_ctx, scale,
+                                                  num_seqs, num_heads, g, ws, stream, k_scale,
+                                                  v_scale);
+}
+
+template <typename T, int D, int BS, int G>
 hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void* vc,
                            const uint32_t* bt, int32_t bts, const uint32_t* cl, int32_t max_ctx,
                            float scale, int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
-                           const DecodeWorkspace& ws, hipStream_t stream) {
+                           const DecodeWorkspace& ws, hipStream_t stream, const float*,
+                           const float*) {
   const int max_parts = (max_ctx + kPT - 1) / kPT;
   dim3 grid((unsigned)g.num_kv_heads, (unsigned)num_seqs, (unsigned)(max_parts > 0 ? max_parts : 1));
   hipLaunchKernelGGL((paged_decode_kernel<T, D, BS, G>), grid, dim3(64), 0, stream,
@@ -833,6 +929,25 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (D == 256 && BS == 8) { VPA_DECODE_G(T, 256, 8) }      \
   if (D == 256 && BS == 16) { VPA_DECODE_G(T, 256, 16) }    \
   if (D == 256 && BS == 32) { VPA_DECODE_G(T, 256, 32) }
+
+#define VPA_DECODE_FP8_G(T, D, BS)                                       \
+  if (group == 1) return launch_decode_rows_fp8<T, D, BS, 1>(args...);   \
+  if (group == 2) return launch_decode_rows_fp8<T, D, BS, 2>(args...);   \
+  if (group == 4) return launch_decode_rows_fp8<T, D, BS, 4>(args...);
+
+#define VPA_DECODE_FP8_DBS(T)                                  \
+  if (D == 64 && BS == 16) { VPA_DECODE_FP8_G(T, 64, 16) }     \
+  if (D == 64 && BS == 32) { VPA_DECODE_FP8_G(T, 64, 32) }     \
+  if (D == 128 && BS == 16) { VPA_DECODE_FP8_G(T, 128, 16) }   \
+  if (D == 128 && BS == 32) { VPA_DECODE_FP8_G(T, 128, 32) }
+
+// fp8 caches: the rows kernel for bf16 / f16 queries.
+template <typename... A>
+hipError_t dispatch_decode_fp8(int dtype, int D, int BS, int group, A... args) {
+  if (dtype == VPA_DTYPE_BF16) { VPA_DECODE_FP8_DBS(bf16_t) }
+  if (dtype == VPA_DTYPE_F16) { VPA_DECODE_FP8_DBS(f16_t) }
+  return hipErrorInvalidValue;
+}
 
 template <typename... A>
 hipError_t dispatch_decode(int dtype, int D, int BS, int group, A... args) {
@@ -906,16 +1021,23 @@ DecodeWorkspace carve_decode_workspace(void* base, int num_seqs, int num_heads, 
   return ws;
 }
 
-hipError_t launch_paged_decode(int dtype, void* out, const void* query, const void* key_cache,
-                               const void* value_cache, const uint32_t* block_tables,
-                               int32_t block_table_stride, const uint32_t* context_lens,
-                               int32_t max_context_len, float scale, int32_t num_seqs,
-                               int32_t num_heads, const CacheGeom& g, const DecodeWorkspace& ws,
-                               hipStream_t stream) {
+hipError_t launch_paged_decode(int dtype, int cache_dtype, void* out, const void* query,
+                               const void* key_cache, const void* value_cache,
+                               const uint32_t* block_tables, int32_t block_table_stride,
+                               const uint32_t* context_lens, int32_t max_context_len,
+                               float scale, const float* k_scale, const float* v_scale,
+                               int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
+                               const DecodeWorkspace& ws, hipStream_t stream) {
   const int group = num_heads / g.num_kv_heads;
+  if (cache_dtype == VPA_DTYPE_FP8_E4M3)
+    return dispatch_decode_fp8(dtype, g.head_dim, g.block_size, group, out, query, key_cache,
+                               value_cache, block_tables, block_table_stride, context_lens,
+                               max_context_len, scale, num_seqs, num_heads, g, ws, stream,
+                               k_scale, v_scale);
   return dispatch_decode(dtype, g.head_dim, g.block_size, group, out, query, key_cache,
                          value_cache, block_tables, block_table_stride, context_lens,
-                         max_context_len, scale, num_seqs, num_heads, g, ws, stream);
+                         max_context_len, scale, num_seqs, num_heads, g, ws, stream, k_scale,
+                         v_scale);
 }
 
 }  // namespace vpa

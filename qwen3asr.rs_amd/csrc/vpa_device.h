@@ -15,6 +15,11 @@ struct bf16_t {
 struct f16_t {
   uint16_t x;
 };
+// One byte of an fp8 (OCP E4M3FN) cache: bias 7, no infinities, S.1111.111
+// is NaN, largest finite 448.
+struct fp8_t {
+  uint8_t x;
+};
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
 typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2_t;
@@ -32,6 +37,10 @@ struct ElemTraits<bf16_t> {
 template <>
 struct ElemTraits<f16_t> {
   static constexpr int kBytes = 2;
+};
+template <>
+struct ElemTraits<fp8_t> {
+  static constexpr int kBytes = 1;
 };
 
 // Elements per 16-byte vector: the key-cache pack factor x of the layout.
@@ -60,6 +69,62 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   _Float16 v = (_Float16)f;
   return __builtin_bit_cast(uint16_t, v);
+}
+
+// One element of T widened to f32 (exact).
+template <typename T>
+__device__ __forceinline__ float load_as_f32(const T* p);
+template <>
+__device__ __forceinline__ float load_as_f32<float>(const float* p) {
+  return *p;
+}
+template <>
+__device__ __forceinline__ float load_as_f32<bf16_t>(const bf16_t* p) {
+  return bf16_bits_to_f32(p->x);
+}
+template <>
+__device__ __forceinline__ float load_as_f32<f16_t>(const f16_t* p) {
+  return f16_bits_to_f32(p->x);
+}
+
+// f32 -> E4M3FN byte: round to nearest even, |x| >= 448 and infinities
+// saturate to +-448, NaN gives S.1111.111 (the quantising rule of fp8 KV
+// caches). Written out bit by bit so it matches the CPU restatement exactly.
+__device__ __forceinline__ uint32_t fp8_from_f32(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  if (a >= 0x43e00000u) return sign | 0x7eu;
+  if (a < 0x3c800000u)  // below 2^-6: multiples of 2^-9, rint rounds half to even
+    return sign | (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  return sign | ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
+}
+
+// Two E4M3FN bytes (byte pair `hi` of a word) -> two packed 16-bit values of
+// T (bf16 or f16; exact: every E4M3 value is representable), gfx950's
+// v_cvt_scalef32_pk_{bf16,f16}_fp8 with scale 1.
+template <typename T>
+__device__ __forceinline__ uint32_t fp8x2_to_pk(uint32_t w, bool hi);
+template <>
+__device__ __forceinline__ uint32_t fp8x2_to_pk<bf16_t>(uint32_t w, bool hi) {
+  return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true))
+            : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+}
+template <>
+__device__ __forceinline__ uint32_t fp8x2_to_pk<f16_t>(uint32_t w, bool hi) {
+  return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true))
+            : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+// Sixteen E4M3FN bytes -> sixteen values of T in two 16-byte vectors
+// (lo: bytes 0..7, hi: bytes 8..15).
+template <typename T>
+__device__ __forceinline__ void fp8x16_to_pk(const uint4& v, uint4& lo, uint4& hi) {
+  lo = make_uint4(fp8x2_to_pk<T>(v.x, false), fp8x2_to_pk<T>(v.x, true),
+                  fp8x2_to_pk<T>(v.y, false), fp8x2_to_pk<T>(v.y, true));
+  hi = make_uint4(fp8x2_to_pk<T>(v.z, false), fp8x2_to_pk<T>(v.z, true),
+                  fp8x2_to_pk<T>(v.w, false), fp8x2_to_pk<T>(v.w, true));
 }
 
 template <typename T>

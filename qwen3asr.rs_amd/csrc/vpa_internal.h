@@ -54,24 +54,33 @@ DecodeWorkspace carve_decode_workspace(void* base, int num_seqs, int num_heads, 
 
 // Launchers return hipSuccess or the launch error. Arguments are validated by
 // the caller.
-hipError_t launch_reshape_and_cache(int dtype, const void* key, const void* value,
-                                    int64_t key_token_stride, int64_t value_token_stride,
-                                    void* key_cache, void* value_cache,
-                                    const int64_t* slot_mapping, int64_t num_tokens,
-                                    const CacheGeom& g, hipStream_t stream);
+// cache_dtype is dtype (bit-exact copy) or VPA_DTYPE_FP8_E4M3 (quantised
+// with the device scalars *k_scale / *v_scale).
+hipError_t launch_reshape_and_cache(int dtype, int cache_dtype, const void* key,
+                                    const void* value, int64_t key_token_stride,
+                                    int64_t value_token_stride, void* key_cache,
+                                    void* value_cache, const int64_t* slot_mapping,
+                                    int64_t num_tokens, const CacheGeom& g, const float* k_scale,
+                                    const float* v_scale, hipStream_t stream);
 
-hipError_t launch_gather_kv_cache(int dtype, void* out_key, void* out_value,
-                                  const void* key_cache, const void* value_cache,
-                                  const uint32_t* block_tables, int32_t block_table_stride,
-                                  const uint32_t* cu_seqlens, int32_t num_seqs,
-                                  const CacheGeom& g, hipStream_t stream);
+// out_dtype is cache_dtype (copy) or, for an fp8 cache, f32 / f16 / bf16
+// (dequantised with *k_scale / *v_scale).
+hipError_t launch_gather_kv_cache(int cache_dtype, int out_dtype, void* out_key,
+                                  void* out_value, const void* key_cache,
+                                  const void* value_cache, const uint32_t* block_tables,
+                                  int32_t block_table_stride, const uint32_t* cu_seqlens,
+                                  int32_t num_seqs, const CacheGeom& g, const float* k_scale,
+                                  const float* v_scale, hipStream_t stream);
 
-hipError_t launch_paged_decode(int dtype, void* out, const void* query, const void* key_cache,
-                               const void* value_cache, const uint32_t* block_tables,
-                               int32_t block_table_stride, const uint32_t* context_lens,
-                               int32_t max_context_len, float scale, int32_t num_seqs,
-                               int32_t num_heads, const CacheGeom& g, const DecodeWorkspace& ws,
-                               hipStream_t stream);
+// cache_dtype is dtype, or VPA_DTYPE_FP8_E4M3 with a bf16 / f16 query
+// (scales are device pointers, read only for fp8).
+hipError_t launch_paged_decode(int dtype, int cache_dtype, void* out, const void* query,
+                               const void* key_cache, const void* value_cache,
+                               const uint32_t* block_tables, int32_t block_table_stride,
+                               const uint32_t* context_lens, int32_t max_context_len,
+                               float scale, const float* k_scale, const float* v_scale,
+                               int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
+                               const DecodeWorkspace& ws, hipStream_t stream);
 
 hipError_t launch_prefill_paged(int dtype, void* out, const void* query, const void* key_cache,
                                 const void* value_cache, const uint32_t* block_tables,

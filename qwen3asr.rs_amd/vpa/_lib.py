@@ -25,6 +25,7 @@ VPA_ERR_NOT_FOUND = 6
 DTYPE_F32 = 0
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
+DTYPE_FP8_E4M3 = 3  # cache element only (OCP E4M3FN bytes)
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32

@@ -31,6 +31,9 @@ _DTYPES = {
     torch.float32: _lib.DTYPE_F32,
     torch.float16: _lib.DTYPE_F16,
     torch.bfloat16: _lib.DTYPE_BF16,
+    # fp8 caches: E4M3FN bytes, as torch's float8 type or raw uint8
+    torch.float8_e4m3fn: _lib.DTYPE_FP8_E4M3,
+    torch.uint8: _lib.DTYPE_FP8_E4M3,
 }
 
 
@@ -100,8 +103,9 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_scale: Optional[
     """Scatter ``key``/``value`` [T, KVH, D] into the caches at ``slot_mapping`` (i64).
 
     Negative slots are padding and are skipped. The caches are written in
-    place. ``k_scale``/``v_scale`` are accepted for signature parity and
-    ignored (no fp8 cache in this build)."""
+    place. For 16/32-bit caches ``k_scale``/``v_scale`` are ignored; an fp8
+    cache (``torch.float8_e4m3fn`` or ``uint8``) stores E4M3FN(x / scale)
+    with the one-element f32 device tensors ``k_scale``/``v_scale``."""
     _require_device(key, value, key_cache, value_cache, slot_mapping)
     nb, kvh, d, bs, bstride, hstride = cache_geometry(key_cache, value_cache)
     if key.dim() != 3 or value.shape != key.shape:

@@ -243,3 +243,68 @@ def test_paged_attention_planned_validates_like_paged_attention():
         msg_b = lib.vpa_last_error().decode()
         assert rc_a == rc_b != 0
         assert msg_b.replace("paged_attention_planned", "paged_attention") == msg_a
+
+
+# ---- fp8 (E4M3FN) caches -------------------------------------------------------
+
+FP8 = _lib.DTYPE_FP8_E4M3
+F8_STRIDES = dict(bstride=8 * 128 * 16, hstride=128 * 16)  # in bytes = elements
+
+
+def test_cache_layout_fp8_packs_16():
+    rc, ks, vs = layout(8, 128, 16, 100, FP8)
+    assert rc == 0 and ks == (100, 8, 8, 16, 16) and vs == (100, 8, 128, 16)
+    rc, _, _ = layout(8, 72, 16, 100, FP8)
+    assert rc == _lib.VPA_ERR_INVALID_ARGUMENT  # 72 is not a multiple of 16
+
+
+@pytest.mark.parametrize("over,code,needle", [
+    (dict(cdtype=FP8, **F8_STRIDES), _lib.VPA_ERR_INVALID_ARGUMENT, "k_scale and v_scale"),
+    (dict(cdtype=FP8, ks=FAKE, **F8_STRIDES), _lib.VPA_ERR_INVALID_ARGUMENT, "k_scale and v_scale"),
+    (dict(cdtype=FP8, ks=FAKE + 2, vs=FAKE, **F8_STRIDES), _lib.VPA_ERR_INVALID_ARGUMENT,
+     "4-byte aligned"),
+    (dict(dtype=FP8, cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES), _lib.VPA_ERR_UNSUPPORTED,
+     "input dtype"),
+])
+def test_reshape_and_cache_fp8_validation(over, code, needle):
+    rc, msg = rc_call(**over)
+    assert rc == code, msg
+    assert needle in msg
+
+
+@pytest.mark.parametrize("dtype", [_lib.DTYPE_F32, _lib.DTYPE_F16, _lib.DTYPE_BF16])
+def test_reshape_and_cache_fp8_accepts_every_float_input(dtype):
+    # validation passes up to the launch, which a GPU-less host cannot do:
+    # only the HIP status may fail (never an argument or support error)
+    rc, msg = rc_call(dtype=dtype, cdtype=FP8, ks=FAKE, vs=FAKE, t=0, **F8_STRIDES)
+    assert rc == 0, msg
+
+
+@pytest.mark.parametrize("over,code,needle", [
+    (dict(cdtype=FP8, **F8_STRIDES), _lib.VPA_ERR_INVALID_ARGUMENT, "k_scale and v_scale"),
+    (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES),
+     _lib.VPA_ERR_UNSUPPORTED, "differs"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bstride=8 * 128 * 8, hstride=128 * 8),
+     _lib.VPA_ERR_UNSUPPORTED, "block_size 16 or 32"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bstride=8 * 256 * 16, hstride=256 * 16),
+     _lib.VPA_ERR_UNSUPPORTED, "head_dim 64 or 128"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES), _lib.VPA_ERR_WORKSPACE, "workspace"),
+])
+def test_paged_attention_fp8_validation(over, code, needle):
+    rc, msg = pa_call(**over)
+    assert rc == code, msg
+    assert needle in msg
+
+
+def test_gather_and_prefill_fp8_validation():
+    lib = _lib.load()
+    args = [FAKE, FAKE, FAKE, FAKE, None, None, FAKE, 4, FAKE, 2, 10, 8, 128, 16, 100,
+            8 * 128 * 16, 128 * 16, FP8, _lib.DTYPE_BF16, None]
+    assert lib.vpa_gather_kv_cache(*args) == _lib.VPA_ERR_INVALID_ARGUMENT  # no scales
+    assert "k_scale" in lib.vpa_last_error().decode()
+    args[4], args[5], args[17], args[18] = FAKE, FAKE, _lib.DTYPE_BF16, _lib.DTYPE_F32
+    assert lib.vpa_gather_kv_cache(*args) == _lib.VPA_ERR_UNSUPPORTED  # 16-bit cache -> other
+    args[17], args[18], args[9] = FP8, FP8, 0  # fp8 -> fp8 (raw bytes), empty batch
+    assert lib.vpa_gather_kv_cache(*args) == 0, lib.vpa_last_error().decode()
+    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE)
+    assert rc == _lib.VPA_ERR_UNSUPPORTED and "differs" in msg

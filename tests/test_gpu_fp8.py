@@ -1,0 +1,199 @@
+"""GPU parity of the FP8 (E4M3FN) KV cache against the CPU oracle.
+
+* reshape_and_cache into an fp8 cache: bit-exact bytes against the oracle's
+  encode (round to nearest even of x / scale, saturation at 448, NaN kept),
+  for f32 / f16 / bf16 rows, scale 1 and others, decode and prefill slot
+  patterns;
+* gather_kv_cache out of an fp8 cache holding every one of the 256 codes:
+  bit-exact against the oracle's dequantisation byte * scale for f32, f16
+  and bf16 outputs (this pins the device conversion instructions the decode
+  kernel shares);
+* paged_attention over an fp8 cache: the fp64 oracle over the dequantised
+  cache (the reference's fp8 semantics, prefill_paged_attn.metal:698-769),
+  bf16/f16 tolerance 2e-2, with stale NaN bytes past each context.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import vpa
+from oracle import oracle as orc
+from tests._util import (TORCH, assert_attention_close, block_tables_for, i64, random_words,
+                         to_dev, to_host, u32)
+
+pytestmark = pytest.mark.gpu
+
+
+def f8(a: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)).to(device).view(
+        torch.float8_e4m3fn)
+
+
+def f8_host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def scalar(v: float, device) -> torch.Tensor:
+    return torch.tensor([v], dtype=torch.float32, device=device)
+
+
+def spread_values(rng, shape):
+    """Normal values with a tail of large (saturating), tiny (subnormal in
+    E4M3) and special values."""
+    x = (rng.standard_normal(shape) * 20).astype(np.float32)
+    flat = x.reshape(-1)
+    n = flat.size
+    idx = rng.choice(n, size=max(n // 50, 8), replace=False)
+    flat[idx[0::4]] = (rng.standard_normal(len(idx[0::4])) * 1000).astype(np.float32)
+    flat[idx[1::4]] = (rng.standard_normal(len(idx[1::4])) * 1e-3).astype(np.float32)
+    flat[idx[2]] = np.inf
+    flat[idx[3]] = -np.inf
+    flat[idx[5]] = np.nan
+    return x
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16, orc.F32])
+@pytest.mark.parametrize("scales", [(1.0, 1.0), (0.37, 3.1)])
+@pytest.mark.parametrize("pattern", ["decode", "prefill"])
+def test_fp8_append_bit_exact(device, code, scales, pattern):
+    rng = np.random.default_rng(100 * code + int(10 * scales[0]) + (pattern == "decode"))
+    kvh, d, bs, nb = 8, 128, 16, 64
+    ks, vs = scales
+    kc = rng.integers(0, 256, size=(nb, kvh, d // 16, bs, 16), dtype=np.uint8)
+    vc = rng.integers(0, 256, size=(nb, kvh, d, bs), dtype=np.uint8)
+    if pattern == "decode":  # one token per sequence, each alone in its block
+        t = 40
+        slots = rng.choice(nb, size=t, replace=False).astype(np.int64) * bs + rng.integers(
+            0, bs, size=t)
+        slots[::7] = -1  # padding rows
+    else:  # runs through blocks, not block-aligned
+        t = 5 * bs + 3
+        blocks = rng.choice(nb, size=7, replace=False)
+        pos = np.arange(t) + 5
+        slots = blocks[pos // bs].astype(np.int64) * bs + pos % bs
+    kf = spread_values(rng, (t, kvh, d))
+    vf = spread_values(rng, (t, kvh, d))
+    k = kf if code == orc.F32 else orc.from_f32(kf, code)
+    v = vf if code == orc.F32 else orc.from_f32(vf, code)
+    kcd, vcd = f8(kc, device), f8(vc, device)
+    vpa.reshape_and_cache(to_dev(k, code, device), to_dev(v, code, device), scalar(ks, device),
+                          scalar(vs, device), kcd, vcd, i64(slots, device))
+    torch.cuda.synchronize()
+    orc.reshape_and_cache_fp8(k, v, kc, vc, slots, code, ks, vs)
+    np.testing.assert_array_equal(f8_host(kcd), kc)
+    np.testing.assert_array_equal(f8_host(vcd), vc)
+
+
+@pytest.mark.parametrize("out", [orc.F32, orc.F16, orc.BF16])
+@pytest.mark.parametrize("scales", [(1.0, 1.0), (0.5, 3.0)])
+def test_fp8_gather_every_code_bit_exact(device, out, scales):
+    ks, vs = scales
+    rng = np.random.default_rng(11 + out)
+    kvh, d, bs, nb = 2, 128, 16, 24
+    # every byte value appears in both caches
+    kc = rng.permutation(np.resize(np.arange(256, dtype=np.uint8), nb * kvh * d * bs)).reshape(
+        nb, kvh, d // 16, bs, 16)
+    vc = rng.permutation(np.resize(np.arange(256, dtype=np.uint8), nb * kvh * d * bs)).reshape(
+        nb, kvh, d, bs)
+    lens = np.array([37, 1, 16, 130], dtype=np.uint32)
+    bt = block_tables_for(rng, lens, nb, bs)
+    bt[1, 0] = nb + 5  # an absent block gives zero rows
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    gk, gv = vpa.gather_kv_cache(f8(kc, device), f8(vc, device), scalar(ks, device),
+                                 scalar(vs, device), u32(bt, device), u32(cu, device), TORCH[out])
+    torch.cuda.synchronize()
+    wk, wv = orc.gather_kv_cache_fp8(kc, vc, bt, cu, out, ks, vs)
+    for got, want in ((to_host(gk), wk), (to_host(gv), wv)):
+        gf = got if out == orc.F32 else orc.to_f32(got, out)
+        wf = want if out == orc.F32 else orc.to_f32(want, out)
+        assert np.array_equal(np.isnan(gf), np.isnan(wf))
+        fin = ~np.isnan(wf)
+        np.testing.assert_array_equal(got[fin], want[fin])
+
+
+def fp8_decode_case(device, code, h, kvh, d, bs, lens, seed, scales=(1.0, 1.0), planned=False):
+    rng = np.random.default_rng(seed)
+    ks, vs = scales
+    need = sum((int(L) + bs - 1) // bs for L in lens)
+    nb = need + 8
+    kc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d // 16, bs, 16)) * 2).astype(np.float32))
+    vc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d, bs)) * 2).astype(np.float32))
+    bt = block_tables_for(rng, [max(int(L), 1) for L in lens], nb, bs)
+    # stale NaN bytes past every context in its last block
+    for s, L in enumerate(lens):
+        if L % bs:
+            blk = bt[s, (L - 1) // bs]
+            kc[blk, :, :, L % bs:, :] = 0x7F
+            vc[blk, :, :, L % bs:] = 0x7F
+    q = random_words(rng, (len(lens), h, d), code)
+    lens = np.asarray(lens, dtype=np.uint32)
+    max_ctx = int(lens.max())
+    scale = d ** -0.5
+    args = (to_dev(q, code, device), scalar(ks, device), scalar(vs, device), f8(kc, device),
+            f8(vc, device), u32(bt, device), u32(lens, device), None, max_ctx, scale, 1.0, None)
+    if planned:
+        ws = vpa.paged_attention_workspace(len(lens), h, d, max_ctx, device)
+        vpa.paged_attention_plan(args[6], max_ctx, bt.shape[1], h, args[3], args[4], TORCH[code],
+                                 ws)
+        out = vpa.paged_attention(*args, workspace=ws, planned=True)
+    else:
+        out = vpa.paged_attention(*args)
+    torch.cuda.synchronize()
+    want = orc.paged_attention(q, kc, vc, bt, lens, max_ctx, scale, dtype=code,
+                               kv_dtype=orc.FP8, k_scale=ks, v_scale=vs)
+    return orc.to_f32(to_host(out), code), want
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("bs", [16, 32])
+def test_fp8_decode_qwen3_asr_shape(device, code, bs):
+    lens = [1, 2, 15, 16, 17, 100, 255, 256, 257, 1023, 1024, 1025, 2600]
+    got, want = fp8_decode_case(device, code, 16, 8, 128, bs, lens, seed=bs + code)
+    assert_attention_close(got, want, code, f"fp8 code={code} bs={bs}")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("h,kvh", [(8, 8), (16, 8), (16, 4)])
+def test_fp8_decode_head_dims_and_groups(device, d, h, kvh):
+    got, want = fp8_decode_case(device, orc.BF16, h, kvh, d, 16, [3, 64, 300, 1500],
+                                seed=d + h + kvh)
+    assert_attention_close(got, want, orc.BF16, f"fp8 d={d} h={h} kvh={kvh}")
+
+
+@pytest.mark.parametrize("scales", [(0.37, 3.1), (4.0, 0.25)])
+def test_fp8_decode_scales_and_planned(device, scales):
+    lens = [5, 700, 1100, 2049]
+    got, want = fp8_decode_case(device, orc.BF16, 16, 8, 128, 16, lens, seed=77, scales=scales,
+                                planned=True)
+    assert_attention_close(got, want, orc.BF16, f"fp8 scales={scales}")
+
+
+def test_fp8_append_then_decode_end_to_end(device):
+    """bf16 rows appended into an fp8 cache and attended: the same as the
+    oracle's append followed by its fp8 attention."""
+    rng = np.random.default_rng(3)
+    h, kvh, d, bs = 16, 8, 128, 16
+    lens = [1, 33, 500, 1030]
+    nb = sum((L + bs - 1) // bs for L in lens) + 4
+    kc = np.zeros((nb, kvh, d // 16, bs, 16), np.uint8)
+    vc = np.zeros((nb, kvh, d, bs), np.uint8)
+    bt = block_tables_for(rng, lens, nb, bs)
+    slots = np.concatenate([bt[s, np.arange(L) // bs].astype(np.int64) * bs + np.arange(L) % bs
+                            for s, L in enumerate(lens)])
+    tot = int(sum(lens))
+    k = random_words(rng, (tot, kvh, d), orc.BF16)
+    v = random_words(rng, (tot, kvh, d), orc.BF16)
+    kcd, vcd = f8(kc, device), f8(vc, device)
+    one = scalar(1.0, device)
+    vpa.reshape_and_cache(to_dev(k, orc.BF16, device), to_dev(v, orc.BF16, device), one, one,
+                          kcd, vcd, i64(slots, device))
+    q = random_words(rng, (len(lens), h, d), orc.BF16)
+    out = vpa.paged_attention(to_dev(q, orc.BF16, device), one, one, kcd, vcd, u32(bt, device),
+                              u32(lens, device), None, max(lens), d ** -0.5, 1.0, None)
+    torch.cuda.synchronize()
+    orc.reshape_and_cache_fp8(k, v, kc, vc, slots, orc.BF16, 1.0, 1.0)
+    np.testing.assert_array_equal(f8_host(kcd), kc)
+    want = orc.paged_attention(q, kc, vc, bt, np.array(lens), max(lens), d ** -0.5,
+                               dtype=orc.BF16, kv_dtype=orc.FP8)
+    assert_attention_close(orc.to_f32(to_host(out), orc.BF16), want, orc.BF16, "fp8 e2e")
