@@ -57,6 +57,8 @@ def parse():
                     help="time the step as eager launches instead of a HIP graph replay")
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="skip the c4 chunked-prefill measurement")
+    ap.add_argument("--no-fp8", dest="fp8", action="store_false",
+                    help="skip the fp8-cache decode measurement")
     return ap.parse_args()
 
 
@@ -212,6 +214,63 @@ def cpu_baseline(w, layers, budget_s):
     }
 
 
+def decode_fp8(w, dev, reps):
+    """The decode-only region of the step over fp8 (E4M3FN) caches: the same
+    block tables, lengths and bf16 queries, K/V bytes halved; plan once, then
+    the planned call per layer. Returns GB/s of the fp8 op's algorithmic
+    bytes and its fraction of the HBM peak."""
+    import numpy as np
+    import torch
+
+    import vpa
+
+    B, H, KVH, D, BS = w.num_seqs, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    g = torch.Generator(device=dev)
+    g.manual_seed(w.seed + 1)
+    one = torch.ones(1, dtype=torch.float32, device=dev)
+
+    def fp8_cache(shape):
+        b = torch.randint(0, 256, shape, generator=g, device=dev, dtype=torch.uint8)
+        b[(b & 0x7F) == 0x7F] = 0x38  # no NaN codes
+        return b.view(torch.float8_e4m3fn)
+
+    layers = []
+    pool = None
+    for layer in w.layers:
+        if pool is None or not w.shared_pool:
+            pool = (fp8_cache((layer.num_blocks, KVH, D // 16, BS, 16)),
+                    fp8_cache((layer.num_blocks, KVH, D, BS)))
+        layers.append(dict(kc=pool[0], vc=pool[1],
+                           q=torch.randn((B, H, D), generator=g, device=dev, dtype=torch.bfloat16),
+                           out=torch.empty((B, H, D), device=dev, dtype=torch.bfloat16),
+                           bt=torch.from_numpy(layer.block_tables).to(dev)))
+    ctx = torch.from_numpy(w.context_lens).to(dev)
+    ws = vpa.paged_attention_workspace(B, H, D, w.max_context_len, dev)
+    scale = D ** -0.5
+
+    def run():
+        L0 = layers[0]
+        vpa.paged_attention_plan(ctx, w.max_context_len, L0["bt"].shape[1], H, L0["kc"],
+                                 L0["vc"], torch.bfloat16, ws)
+        for L in layers:
+            vpa.paged_attention(L["q"], one, one, L["kc"], L["vc"], L["bt"], ctx, None,
+                                w.max_context_len, scale, 1.0, None, out=L["out"],
+                                workspace=ws, planned=True)
+
+    for _ in range(2):
+        run()
+    ms = timed_ms(run, reps) / len(layers)
+    lens = w.context_lens.astype(np.int64)
+    per = (lens * 2 * KVH * D + 2 * H * D * 2 + 4 * ((lens + BS - 1) // BS) + 4)
+    nbytes = int(per.sum())
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    del layers, ws
+    torch.cuda.empty_cache()
+    return {"workload": w.name, "cache": "fp8_e4m3 (k_scale = v_scale = 1)", "query": "bf16",
+            "us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes_per_launch": nbytes,
+            "gbps": round(gbps, 2), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
 def prefill_c4(dev, reps=10):
     """Row a3 measured alongside the headline: c4 (64 sequences x 512 new
     tokens over 0..1024 prior tokens, bf16) append with reshape_and_cache,
@@ -344,10 +403,13 @@ def main():
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(w, layers, args.cpu_seconds)
+    del layers, ws
+    torch.cuda.empty_cache()
+    f8 = None
+    if args.fp8 and w.dtype == "bf16":
+        f8 = decode_fp8(w, dev, args.steps)
     pf = None
     if args.prefill:
-        del layers, ws
-        torch.cuda.empty_cache()
         pf = prefill_c4(dev)
 
     line = {
@@ -396,6 +458,7 @@ def main():
             "us_per_launch": round(dec_launch_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
+        "decode_fp8": f8,
         "prefill_c4": pf,
     }
     print(json.dumps(line), flush=True)
