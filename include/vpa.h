@@ -254,6 +254,44 @@ int vpa_chunked_prefill_paged_attention(
     int32_t head_dim, int32_t block_size, int64_t num_blocks, int64_t cache_block_stride,
     int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype, void* stream);
 
+/*
+ * argmax_rows — next-token ids of a batch of logits rows, left on the device.
+ * Replaces argmax_token_ids_from_logits(logits, batch)
+ * (vasr-models/src/model/generation.rs:443-460: candle argmax over dim 1,
+ * then a host read-back of every id), called after each decode forward at
+ * vasr-models/src/model/paged_batch_engine.rs:722 and after prefill at :580.
+ *
+ * logits: [num_rows, row_stride] elements of dtype (f32, f16, bf16), the
+ * first `vocab` of each row used. out_ids[r] (u32, device) is the index of
+ * the first maximum of row r; NaN values are never chosen, except that a
+ * NaN at index 0 gives 0 (candle's left-to-right strictly-greater scan). No
+ * host synchronisation; safe under stream capture.
+ */
+int vpa_argmax_rows(const void* logits, int64_t row_stride, int32_t vocab, int32_t num_rows,
+                    int32_t dtype, uint32_t* out_ids, void* stream);
+
+/*
+ * decode_consume_tokens — the step-start next-token bookkeeping of the
+ * decode loop, on the device. Replaces the host loop of
+ * paged_batch_decode_step (vasr-models/src/model/paged_batch_engine.rs:
+ * 640-667) that reads the pending ids back: for each row r that is not
+ * finished, the pending id next_ids[r] either is an EOS id (one of
+ * eos_ids[0..num_eos)) and the row becomes finished, or it is appended to
+ * the row's generated list (generated[r, gen_len[r]++], a [num_rows,
+ * gen_capacity] u32 buffer; a full list is not extended) and becomes the
+ * row's next input id. Finished rows feed eos_fill_id (the reference pads
+ * with eos_token_ids[0], paged_batch_engine.rs:193-195) instead of being
+ * compacted out of the batch, so a captured decode graph keeps its shape.
+ * input_ids[r] receives the row's input id; *active_count the number of rows
+ * that fed a real token (the 4 bytes a host loop reads when it checks for
+ * completion). finished is u8 per row. All pointers are device memory; no
+ * host synchronisation; safe under stream capture.
+ */
+int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished, uint32_t* generated,
+                              uint32_t* gen_len, int32_t gen_capacity, const uint32_t* eos_ids,
+                              int32_t num_eos, uint32_t eos_fill_id, uint32_t* input_ids,
+                              uint32_t* active_count, int32_t num_rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

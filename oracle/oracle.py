@@ -78,6 +78,11 @@ def lib():
                                                       _i32, _p, _p, _i32, _i32, _dbl, _i32, _i32,
                                                       _i32, _i32, _i64, _i64, _i64, _dbl]
         L.oracle_prefill_attention_kv_f64.restype = None
+        L.oracle_argmax_rows.argtypes = [_i32, _p, _i64, _i32, _i32, _p]
+        L.oracle_argmax_rows.restype = None
+        L.oracle_decode_consume_tokens.argtypes = [_p, _p, _p, _p, _i32, _p, _i32,
+                                                   ctypes.c_uint32, _p, _p, _i32]
+        L.oracle_decode_consume_tokens.restype = None
         L.oracle_prefill_attention_f64.argtypes = [_i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i32,
                                                    _i32, _dbl, _i32, _i32, _i32, _i32, _i64,
                                                    _i64, _i64, _dbl]
@@ -275,3 +280,27 @@ def from_f32(a: np.ndarray, code: int) -> np.ndarray:
     if code == F32:
         return np.ascontiguousarray(a, dtype=np.float32)
     return f32_to_bf16_bits(a) if code == BF16 else f32_to_f16_bits(a)
+
+
+def argmax_rows(logits: np.ndarray, dtype=None) -> np.ndarray:
+    """u32 next-token ids of logits [B, V] (candle's argmax scan)."""
+    code = dtype_code(logits, dtype)
+    logits = np.ascontiguousarray(logits)
+    b, v = logits.shape
+    out = np.zeros(b, dtype=np.uint32)
+    lib().oracle_argmax_rows(code, _ptr(logits), v, v, b, _ptr(out))
+    return out
+
+
+def decode_consume_tokens(next_ids, finished, generated, gen_len, eos_ids, eos_fill_id):
+    """In-place step-start bookkeeping; returns (input_ids, active_count)."""
+    b, cap = generated.shape
+    eos = np.ascontiguousarray(eos_ids, dtype=np.uint32)
+    inp = np.zeros(b, dtype=np.uint32)
+    cnt = np.zeros(1, dtype=np.uint32)
+    lib().oracle_decode_consume_tokens(_ptr(np.ascontiguousarray(next_ids, dtype=np.uint32)),
+                                       _ptr(finished), _ptr(generated), _ptr(gen_len), cap,
+                                       _ptr(eos), eos.size, int(eos_fill_id), _ptr(inp),
+                                       _ptr(cnt), b)
+    return inp, int(cnt[0])
+

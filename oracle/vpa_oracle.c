@@ -523,6 +523,67 @@ void oracle_gather_kv_cache_fp8(int out_dtype, void* out_key, void* out_value,
   }
 }
 
+/*
+ * Next-token ids of logits rows, as candle-core 0.10.2 (git rev 5404348,
+ * Cargo.lock:379-381, not vendored) computes argmax over the last dim: a
+ * left-to-right scan from element 0 that moves only on a strictly greater
+ * value, so the first maximum wins and a NaN (never greater, never less)
+ * is only kept when it is element 0. Called by the reference through
+ * argmax_token_ids_from_logits (vasr-models/src/model/generation.rs:443-460).
+ */
+void oracle_argmax_rows(int dtype, const void* logits, int64_t row_stride, int vocab,
+                        int num_rows, uint32_t* out) {
+  for (int r = 0; r < num_rows; ++r) {
+    const int64_t base = (int64_t)r * row_stride;
+    double best = load_elem(logits, dtype, base);
+    uint32_t bi = 0;
+    for (int i = 1; i < vocab; ++i) {
+      const double v = load_elem(logits, dtype, base + i);
+      if (v > best) {
+        best = v;
+        bi = (uint32_t)i;
+      }
+    }
+    out[r] = bi;
+  }
+}
+
+/*
+ * Step-start bookkeeping of paged_batch_decode_step
+ * (vasr-models/src/model/paged_batch_engine.rs:640-667) over per-row state:
+ * a row that is not finished takes its pending id; an EOS id finishes it,
+ * any other id is appended to its generated list (up to gen_capacity) and
+ * becomes its input id. Finished rows get eos_fill_id as input (the
+ * reference's pad id, eos_token_ids[0], paged_batch_engine.rs:193-195).
+ * *active_count = rows that fed a real token.
+ */
+void oracle_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished,
+                                  uint32_t* generated, uint32_t* gen_len, int gen_capacity,
+                                  const uint32_t* eos_ids, int num_eos, uint32_t eos_fill_id,
+                                  uint32_t* input_ids, uint32_t* active_count, int num_rows) {
+  uint32_t active = 0;
+  for (int r = 0; r < num_rows; ++r) {
+    uint32_t feed = eos_fill_id;
+    if (!finished[r]) {
+      const uint32_t tok = next_ids[r];
+      int eos = 0;
+      for (int e = 0; e < num_eos; ++e) eos |= tok == eos_ids[e];
+      if (eos) {
+        finished[r] = 1;
+      } else {
+        if ((int64_t)gen_len[r] < gen_capacity) {
+          generated[(int64_t)r * gen_capacity + gen_len[r]] = tok;
+          gen_len[r] += 1;
+        }
+        feed = tok;
+        ++active;
+      }
+    }
+    input_ids[r] = feed;
+  }
+  *active_count = active;
+}
+
 /* ---------------------------------------------------------------------- */
 /* CPU baseline: the reference's CPU decode path restated in f32.           */
 /* ---------------------------------------------------------------------- */

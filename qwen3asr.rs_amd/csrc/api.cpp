@@ -518,4 +518,49 @@ int vpa_chunked_prefill_paged_attention(
                                              g, static_cast<hipStream_t>(stream)));
 }
 
+int vpa_argmax_rows(const void* logits, int64_t row_stride, int32_t vocab, int32_t num_rows,
+                    int32_t dtype, uint32_t* out_ids, void* stream) {
+  clear_error();
+  const char* op = "argmax_rows";
+  if (!is_float_dtype(dtype))
+    return fail(VPA_ERR_UNSUPPORTED, "%s: unsupported logits dtype %s", op, dtype_name(dtype));
+  if (num_rows < 0 || vocab < 0 || row_stride < vocab)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: bad sizes num_rows=%d vocab=%d row_stride=%lld",
+                op, num_rows, vocab, (long long)row_stride);
+  if (num_rows == 0) return VPA_OK;
+  if (vocab == 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: argmax of an empty row (vocab = 0)", op);
+  if (logits == nullptr || out_ids == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: logits and out_ids must be non-null", op);
+  const int eb = dtype_bytes(dtype);
+  if ((reinterpret_cast<uintptr_t>(logits) % eb) != 0 ||
+      (reinterpret_cast<uintptr_t>(out_ids) & 3u) != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: misaligned pointers", op);
+  return hip_status(op, launch_argmax_rows(dtype, logits, row_stride, vocab, num_rows, out_ids,
+                                           static_cast<hipStream_t>(stream)));
+}
+
+int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished, uint32_t* generated,
+                              uint32_t* gen_len, int32_t gen_capacity, const uint32_t* eos_ids,
+                              int32_t num_eos, uint32_t eos_fill_id, uint32_t* input_ids,
+                              uint32_t* active_count, int32_t num_rows, void* stream) {
+  clear_error();
+  const char* op = "decode_consume_tokens";
+  if (num_rows < 0 || gen_capacity < 0 || num_eos < 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: bad sizes num_rows=%d gen_capacity=%d num_eos=%d", op, num_rows,
+                gen_capacity, num_eos);
+  if (num_eos == 0 || eos_ids == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: eos_token_ids is empty", op);
+  if (active_count == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: active_count must be non-null", op);
+  if (num_rows > 0 && (next_ids == nullptr || finished == nullptr || gen_len == nullptr ||
+                       input_ids == nullptr || (gen_capacity > 0 && generated == nullptr)))
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: state buffers must be non-null", op);
+  return hip_status(op, launch_consume_tokens(next_ids, finished, generated, gen_len,
+                                              gen_capacity, eos_ids, num_eos, eos_fill_id,
+                                              input_ids, active_count, num_rows,
+                                              static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

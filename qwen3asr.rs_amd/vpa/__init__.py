@@ -7,6 +7,8 @@ Hand-written HIP kernels for gfx950 behind the C ABI of ``include/vpa.h``
 
 from ._lib import VpaError  # noqa: F401
 from .ops import (  # noqa: F401
+    DecodeTokenState,
+    argmax_token_ids_from_logits,
     cache_geometry,
     gather_kv_cache,
     paged_attention,
@@ -17,7 +19,9 @@ from .ops import (  # noqa: F401
 )
 
 __all__ = [
+    "DecodeTokenState",
     "VpaError",
+    "argmax_token_ids_from_logits",
     "cache_geometry",
     "gather_kv_cache",
     "paged_attention",

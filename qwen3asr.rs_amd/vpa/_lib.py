@@ -31,6 +31,7 @@ _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _u64 = ctypes.c_uint64
+_u32 = ctypes.c_uint32
 _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
 _cstr = ctypes.c_char_p
@@ -56,6 +57,9 @@ SIGNATURES = {
     "vpa_chunked_prefill_paged_attention": (ctypes.c_int, [
         _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i64, _f32, _i32, _i32,
         _i32, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
+    "vpa_argmax_rows": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p]),
+    "vpa_decode_consume_tokens": (ctypes.c_int, [
+        _p, _p, _p, _p, _i32, _p, _i32, _u32, _p, _p, _i32, _p]),
     # include/vpa_host.h
     "vpa_bytes_per_paged_block": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _p]),
     "vpa_pool_blocks_for_context": (ctypes.c_int, [_i64, _i32, _p]),

@@ -300,3 +300,67 @@ def paged_attention_varlen_prefill(q: torch.Tensor, key_cache: torch.Tensor,
         int(max_context_len), tq, float(scale), int(bool(causal)), h, kvh, d, bs, nb, bstride,
         hstride, dtype_code(q.dtype), dtype_code(key_cache.dtype), _stream(q)))
     return out
+
+
+# ---- next-token selection and EOS state on the device -------------------------
+
+def argmax_token_ids_from_logits(logits: torch.Tensor, *,
+                                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Next-token ids [B] (u32, on the device) of logits [B, V]: the first
+    maximum of each row, NaN handled as candle's argmax (generation.rs:443-460),
+    without the reference's host read-back."""
+    _require_device(logits)
+    if logits.dim() == 1:
+        logits = logits[None, :]
+    if logits.dim() != 2:
+        raise _err(f"logits must be [B, V], got {tuple(logits.shape)}")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    b, v = logits.shape
+    if out is None:
+        out = torch.empty(b, dtype=torch.uint32, device=logits.device)
+    elif out.dtype != torch.uint32 or out.shape != (b,) or not out.is_contiguous():
+        raise _err(f"out must be a contiguous u32 [{b}] tensor")
+    check(_lib.load().vpa_argmax_rows(logits.data_ptr(), logits.stride(0), v, b,
+                                      dtype_code(logits.dtype), out.data_ptr(),
+                                      _stream(logits)))
+    return out
+
+
+class DecodeTokenState:
+    """Device-resident next-token state of a batch decode loop.
+
+    Mirrors the fields of PagedBatchState that the step-start bookkeeping
+    touches (paged_batch_engine.rs:28-42): ``next_ids`` (pending ids),
+    ``finished`` (u8), ``generated`` [B, capacity] with ``gen_len``, plus the
+    ``input_ids`` buffer a captured decode graph reads and the 4-byte
+    ``active_count``."""
+
+    def __init__(self, batch: int, capacity: int, eos_token_ids, device):
+        eos = list(eos_token_ids)
+        if not eos:
+            raise _err("eos_token_ids is empty")
+        self.batch, self.capacity = batch, capacity
+        self.eos_fill_id = int(eos[0])
+        self.eos_ids = torch.tensor(eos, dtype=torch.uint32, device=device)
+        self.next_ids = torch.zeros(batch, dtype=torch.uint32, device=device)
+        self.finished = torch.zeros(batch, dtype=torch.uint8, device=device)
+        self.generated = torch.zeros((batch, max(capacity, 1)), dtype=torch.uint32, device=device)
+        self.gen_len = torch.zeros(batch, dtype=torch.uint32, device=device)
+        self.input_ids = torch.zeros(batch, dtype=torch.uint32, device=device)
+        self.active_count = torch.zeros(1, dtype=torch.uint32, device=device)
+
+    def select(self, logits: torch.Tensor) -> None:
+        """next_ids <- argmax of the step's logits rows (all rows of the batch)."""
+        argmax_token_ids_from_logits(logits, out=self.next_ids)
+
+    def consume(self) -> None:
+        """Step start (paged_batch_engine.rs:640-667): pending EOS ids finish
+        their rows, other pending ids are appended and become input_ids;
+        finished rows feed the EOS fill id."""
+        check(_lib.load().vpa_decode_consume_tokens(
+            self.next_ids.data_ptr(), self.finished.data_ptr(), self.generated.data_ptr(),
+            self.gen_len.data_ptr(), self.capacity, self.eos_ids.data_ptr(),
+            self.eos_ids.numel(), self.eos_fill_id, self.input_ids.data_ptr(),
+            self.active_count.data_ptr(), self.batch, _stream(self.next_ids)))
+

@@ -465,3 +465,71 @@ def test_fp8_attention_equals_attention_over_dequantised_cache(scales):
                                 kv_dtype=orc.FP8, k_scale=ks, v_scale=vs)
     want = orc.prefill_attention(qp, kc16, vc16, bt, lens, cu, 0.1, dtype=orc.BF16)
     np.testing.assert_array_equal(got, want)
+
+
+# ---- next-token selection and EOS state ---------------------------------------
+
+def test_argmax_oracle_matches_numpy_first_maximum():
+    """Without NaN, candle's strictly-greater scan is numpy's argmax (first
+    occurrence of the maximum); ties are planted so the first-wins rule is
+    exercised."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((64, 1000)).astype(np.float32)
+    for r in range(64):
+        m = x[r].max() + 1.0
+        x[r, rng.choice(1000, size=1 + r % 4, replace=False)] = m
+    np.testing.assert_array_equal(orc.argmax_rows(x), np.argmax(x, axis=1))
+    xb = orc.from_f32(x, orc.BF16)  # bf16 rounding creates more ties
+    np.testing.assert_array_equal(orc.argmax_rows(xb, dtype=orc.BF16),
+                                  np.argmax(orc.to_f32(xb, orc.BF16), axis=1))
+
+
+def test_argmax_oracle_nan_and_infinity_rule():
+    x = np.float32([[np.nan, 5, 1], [0, np.nan, 7], [-np.inf] * 3, [np.nan] * 3, [2, 2, np.inf]])
+    np.testing.assert_array_equal(orc.argmax_rows(x), [0, 2, 0, 0, 2])
+
+
+def _reference_decode_loop(pending, steps_logits_ids, eos_ids):
+    """The reference's host loop (paged_batch_engine.rs:640-667 and :722):
+    active rows are compacted; a pending EOS id finishes its row, others are
+    pushed to `generated` and fed; the forward's argmax of the fed rows
+    becomes their pending id."""
+    batch = len(pending)
+    next_ids = list(pending)
+    finished = [False] * batch
+    generated = [[] for _ in range(batch)]
+    for new_ids in steps_logits_ids:
+        forward = [i for i in range(batch) if not finished[i]]
+        fed = []
+        for i in forward:
+            tok = next_ids[i]
+            if tok in eos_ids:
+                finished[i] = True
+                continue
+            generated[i].append(tok)
+            fed.append(i)
+        for i in fed:
+            next_ids[i] = int(new_ids[i])
+    return finished, generated
+
+
+def test_consume_oracle_equals_reference_loop_with_compaction():
+    """Feeding finished rows the fill id instead of compacting them gives the
+    reference's generated lists and finished flags after every step."""
+    rng = np.random.default_rng(9)
+    batch, steps, cap = 37, 12, 16
+    eos = [2, 5]
+    pending = rng.integers(0, 8, size=batch)
+    new_ids = [rng.integers(0, 8, size=batch) for _ in range(steps)]
+    want_fin, want_gen = _reference_decode_loop(list(pending), new_ids, eos)
+    nid = pending.astype(np.uint32)
+    fin = np.zeros(batch, np.uint8)
+    gen = np.zeros((batch, cap), np.uint32)
+    glen = np.zeros(batch, np.uint32)
+    for s in range(steps):
+        inp, active = orc.decode_consume_tokens(nid, fin, gen, glen, eos, eos[0])
+        assert active == int((fin == 0).sum())
+        assert np.all(inp[fin == 1] == eos[0])
+        nid = np.where(fin == 0, new_ids[s], nid).astype(np.uint32)  # forward + argmax
+    assert fin.astype(bool).tolist() == want_fin
+    assert [gen[i, :glen[i]].tolist() for i in range(batch)] == want_gen
