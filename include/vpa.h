@@ -292,6 +292,66 @@ int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished, uint3
                               int32_t num_eos, uint32_t eos_fill_id, uint32_t* input_ids,
                               uint32_t* active_count, int32_t num_rows, void* stream);
 
+/*
+ * Device-resident KV block allocation (the decode loop without per-step
+ * host metadata). State, all device memory, one row per batch slot:
+ *   block_tables [num_rows, block_table_stride] u32  each row's blocks, in order
+ *   row_blocks   [num_rows] u32   blocks the row holds
+ *   positions    [num_rows] u32   position of the row's next token
+ *   free_ring    [free_ring_capacity] u32, free_ring_state [2] u32 = {head,
+ *                count}: the free block ids in hand-out order (a FIFO ring;
+ *                capacity >= the pool's block count)
+ * It restates PagedBlockManager (vasr-models/src/model/paged_cache_runtime.rs:
+ * 217-380: a FIFO free list, initially ids 1..num_blocks-1, handed out from
+ * the front, released blocks pushed to the back last block first, block 0
+ * never) and decode_metadata_for_batch_step (vasr-paged-attn/src/
+ * paged_kv_cache.rs:924-1059). Each call is one launch, safe under stream
+ * capture, with no host synchronisation.
+ */
+
+/*
+ * allocate_rows — grow rows (in index order) to hold target_tokens[r]
+ * tokens: a row takes all the blocks it lacks from the ring's head, or none
+ * when the ring cannot serve it (ok[r] = 0), as try_allocate_slots row by row
+ * (paged_cache_runtime.rs:260-300, paged_batch_engine.rs:209-227). Used to
+ * admit requests after prefill.
+ */
+int vpa_allocate_rows(uint32_t* block_tables, int32_t block_table_stride, uint32_t* row_blocks,
+                      const uint32_t* target_tokens, uint8_t* ok, uint32_t* free_ring,
+                      uint32_t* free_ring_state, int32_t free_ring_capacity, int32_t block_size,
+                      int32_t num_rows, void* stream);
+
+/*
+ * decode_step_metadata — one decode step's metadata: for every row not
+ * finished (finished may be NULL), in index order, a block is taken from the
+ * ring when the row's next token starts one (allocate_slots(prompt_len +
+ * step + 1), paged_batch_engine.rs:629-639), then
+ *   slot_mapping[r] = block_tables[r, pos / BS] * BS + pos % BS,
+ *   context_lens[r] = pos + 1, positions[r] = pos + 1   (pos = positions[r])
+ * as decode_metadata_for_batch_step builds them. A row the ring cannot serve,
+ * a finished row, or a row whose table is too narrow gets slot_mapping
+ * PAD_SLOT_ID (-1) and context_lens 1 and does not advance. status[3] u32 =
+ * {rows stalled for lack of blocks, rows rejected (a row may grow by one
+ * block per step and must fit block_table_stride), largest context_len}.
+ */
+int vpa_decode_step_metadata(uint32_t* block_tables, int32_t block_table_stride,
+                             uint32_t* row_blocks, uint32_t* positions, const uint8_t* finished,
+                             uint32_t* free_ring, uint32_t* free_ring_state,
+                             int32_t free_ring_capacity, int32_t block_size,
+                             int64_t* slot_mapping, uint32_t* context_lens, uint32_t* status,
+                             int32_t num_rows, void* stream);
+
+/*
+ * release_blocks — rows (in index order) keep their first keep_blocks[r]
+ * blocks and give the rest back to the ring's tail, last block first, id 0
+ * never (trim_request_to_num_tokens with keep = ceil(tokens / BS), and
+ * free_request with keep = 0; paged_cache_runtime.rs:330-380).
+ */
+int vpa_release_blocks(const uint32_t* block_tables, int32_t block_table_stride,
+                       uint32_t* row_blocks, const uint32_t* keep_blocks, uint32_t* free_ring,
+                       uint32_t* free_ring_state, int32_t free_ring_capacity, int32_t num_rows,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

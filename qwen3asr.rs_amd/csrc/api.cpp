@@ -563,4 +563,82 @@ int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished, uint3
                                               static_cast<hipStream_t>(stream)));
 }
 
+namespace {
+int check_alloc_state(const char* op, const void* block_tables, int32_t stride,
+                      const void* row_blocks, const void* ring, const void* ring_state,
+                      int32_t ring_cap, int32_t num_rows) {
+  if (num_rows < 0 || stride <= 0 || ring_cap <= 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: bad sizes num_rows=%d block_table_stride=%d free_ring_capacity=%d", op,
+                num_rows, stride, ring_cap);
+  if (ring == nullptr || ring_state == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: free_ring and free_ring_state must be non-null",
+                op);
+  if (num_rows > 0 && (block_tables == nullptr || row_blocks == nullptr))
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: block_tables and row_blocks must be non-null",
+                op);
+  return VPA_OK;
+}
+}  // namespace
+
+int vpa_allocate_rows(uint32_t* block_tables, int32_t block_table_stride, uint32_t* row_blocks,
+                      const uint32_t* target_tokens, uint8_t* ok, uint32_t* free_ring,
+                      uint32_t* free_ring_state, int32_t free_ring_capacity, int32_t block_size,
+                      int32_t num_rows, void* stream) {
+  clear_error();
+  const char* op = "allocate_rows";
+  int rc = check_alloc_state(op, block_tables, block_table_stride, row_blocks, free_ring,
+                             free_ring_state, free_ring_capacity, num_rows);
+  if (rc != VPA_OK) return rc;
+  if (block_size <= 0) return fail(VPA_ERR_INVALID_ARGUMENT, "%s: block_size must be > 0", op);
+  if (num_rows == 0) return VPA_OK;
+  if (target_tokens == nullptr || ok == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: target_tokens and ok must be non-null", op);
+  return hip_status(op, launch_allocate_rows(block_tables, block_table_stride, row_blocks,
+                                             target_tokens, ok, free_ring, free_ring_state,
+                                             free_ring_capacity, block_size, num_rows,
+                                             static_cast<hipStream_t>(stream)));
+}
+
+int vpa_decode_step_metadata(uint32_t* block_tables, int32_t block_table_stride,
+                             uint32_t* row_blocks, uint32_t* positions, const uint8_t* finished,
+                             uint32_t* free_ring, uint32_t* free_ring_state,
+                             int32_t free_ring_capacity, int32_t block_size,
+                             int64_t* slot_mapping, uint32_t* context_lens, uint32_t* status,
+                             int32_t num_rows, void* stream) {
+  clear_error();
+  const char* op = "decode_step_metadata";
+  int rc = check_alloc_state(op, block_tables, block_table_stride, row_blocks, free_ring,
+                             free_ring_state, free_ring_capacity, num_rows);
+  if (rc != VPA_OK) return rc;
+  if (block_size <= 0) return fail(VPA_ERR_INVALID_ARGUMENT, "%s: block_size must be > 0", op);
+  if (status == nullptr) return fail(VPA_ERR_INVALID_ARGUMENT, "%s: status must be non-null", op);
+  if (num_rows > 0 && (positions == nullptr || slot_mapping == nullptr || context_lens == nullptr))
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: positions, slot_mapping and context_lens must be non-null", op);
+  return hip_status(op, launch_decode_step_metadata(
+                            block_tables, block_table_stride, row_blocks, positions, finished,
+                            free_ring, free_ring_state, free_ring_capacity, block_size,
+                            slot_mapping, context_lens, status, num_rows,
+                            static_cast<hipStream_t>(stream)));
+}
+
+int vpa_release_blocks(const uint32_t* block_tables, int32_t block_table_stride,
+                       uint32_t* row_blocks, const uint32_t* keep_blocks, uint32_t* free_ring,
+                       uint32_t* free_ring_state, int32_t free_ring_capacity, int32_t num_rows,
+                       void* stream) {
+  clear_error();
+  const char* op = "release_blocks";
+  int rc = check_alloc_state(op, block_tables, block_table_stride, row_blocks, free_ring,
+                             free_ring_state, free_ring_capacity, num_rows);
+  if (rc != VPA_OK) return rc;
+  if (num_rows == 0) return VPA_OK;
+  if (keep_blocks == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: keep_blocks must be non-null", op);
+  return hip_status(op, launch_release_blocks(block_tables, block_table_stride, row_blocks,
+                                              keep_blocks, free_ring, free_ring_state,
+                                              free_ring_capacity, num_rows,
+                                              static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

@@ -112,6 +112,23 @@ hipError_t launch_consume_tokens(const uint32_t* next_ids, uint8_t* finished,
                                  uint32_t* input_ids, uint32_t* active_count, int32_t num_rows,
                                  hipStream_t stream);
 
+// Device-resident KV block allocation and decode-step metadata.
+hipError_t launch_allocate_rows(uint32_t* block_tables, int32_t cols, uint32_t* row_blocks,
+                                const uint32_t* target_tokens, uint8_t* ok, uint32_t* ring,
+                                uint32_t* ring_state, int32_t ring_cap, int32_t block_size,
+                                int32_t num_rows, hipStream_t stream);
+hipError_t launch_decode_step_metadata(uint32_t* block_tables, int32_t cols,
+                                       uint32_t* row_blocks, uint32_t* positions,
+                                       const uint8_t* finished, uint32_t* ring,
+                                       uint32_t* ring_state, int32_t ring_cap,
+                                       int32_t block_size, int64_t* slot_mapping,
+                                       uint32_t* context_lens, uint32_t* status,
+                                       int32_t num_rows, hipStream_t stream);
+hipError_t launch_release_blocks(const uint32_t* block_tables, int32_t cols,
+                                 uint32_t* row_blocks, const uint32_t* keep_blocks,
+                                 uint32_t* ring, uint32_t* ring_state, int32_t ring_cap,
+                                 int32_t num_rows, hipStream_t stream);
+
 // True when a decode kernel is compiled for this (dtype, head_dim, block_size,
 // query heads per kv head) combination.
 bool decode_supported(int dtype, int head_dim, int block_size, int group);

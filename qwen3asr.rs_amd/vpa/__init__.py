@@ -8,6 +8,7 @@ Hand-written HIP kernels for gfx950 behind the C ABI of ``include/vpa.h``
 from ._lib import VpaError  # noqa: F401
 from .ops import (  # noqa: F401
     DecodeTokenState,
+    DeviceBlockAllocator,
     argmax_token_ids_from_logits,
     cache_geometry,
     gather_kv_cache,
@@ -20,6 +21,7 @@ from .ops import (  # noqa: F401
 
 __all__ = [
     "DecodeTokenState",
+    "DeviceBlockAllocator",
     "VpaError",
     "argmax_token_ids_from_logits",
     "cache_geometry",

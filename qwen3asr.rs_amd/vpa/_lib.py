@@ -60,6 +60,10 @@ SIGNATURES = {
     "vpa_argmax_rows": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p]),
     "vpa_decode_consume_tokens": (ctypes.c_int, [
         _p, _p, _p, _p, _i32, _p, _i32, _u32, _p, _p, _i32, _p]),
+    "vpa_allocate_rows": (ctypes.c_int, [_p, _i32, _p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
+    "vpa_decode_step_metadata": (ctypes.c_int, [
+        _p, _i32, _p, _p, _p, _p, _p, _i32, _i32, _p, _p, _p, _i32, _p]),
+    "vpa_release_blocks": (ctypes.c_int, [_p, _i32, _p, _p, _p, _p, _i32, _i32, _p]),
     # include/vpa_host.h
     "vpa_bytes_per_paged_block": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _p]),
     "vpa_pool_blocks_for_context": (ctypes.c_int, [_i64, _i32, _p]),

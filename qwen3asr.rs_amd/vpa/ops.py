@@ -364,3 +364,61 @@ class DecodeTokenState:
             self.eos_ids.numel(), self.eos_fill_id, self.input_ids.data_ptr(),
             self.active_count.data_ptr(), self.batch, _stream(self.next_ids)))
 
+
+class DeviceBlockAllocator:
+    """Device-resident KV block allocation and decode-step metadata for a
+    fixed batch of rows (``vpa_allocate_rows`` / ``vpa_decode_step_metadata`` /
+    ``vpa_release_blocks``): the PagedBlockManager of
+    paged_cache_runtime.rs:217-380 (FIFO free list of ids 1..num_blocks-1)
+    and decode_metadata_for_batch_step of paged_kv_cache.rs:924-1059, with
+    every buffer on the device so a captured decode graph can run them."""
+
+    def __init__(self, num_blocks: int, block_size: int, batch: int, cols: int, device):
+        import numpy as np
+
+        if num_blocks < 2 or block_size <= 0 or batch < 0 or cols <= 0:
+            raise _err("bad allocator sizes")
+        self.block_size, self.batch, self.cols = block_size, batch, cols
+        self.ring_capacity = num_blocks
+        ring = np.zeros(num_blocks, dtype=np.uint32)
+        ring[:num_blocks - 1] = np.arange(1, num_blocks, dtype=np.uint32)
+        self.free_ring = torch.from_numpy(ring).to(device)
+        self.free_ring_state = torch.tensor([0, num_blocks - 1], dtype=torch.uint32, device=device)
+        self.block_tables = torch.zeros((batch, cols), dtype=torch.uint32, device=device)
+        self.row_blocks = torch.zeros(batch, dtype=torch.uint32, device=device)
+        self.positions = torch.zeros(batch, dtype=torch.uint32, device=device)
+        self.slot_mapping = torch.full((batch,), -1, dtype=torch.int64, device=device)
+        self.context_lens = torch.ones(batch, dtype=torch.uint32, device=device)
+        self.status = torch.zeros(3, dtype=torch.uint32, device=device)
+        self.ok = torch.zeros(batch, dtype=torch.uint8, device=device)
+
+    def _common(self):
+        return (self.free_ring.data_ptr(), self.free_ring_state.data_ptr(), self.ring_capacity)
+
+    def allocate(self, target_tokens: torch.Tensor) -> torch.Tensor:
+        """Grow rows to hold target_tokens[r] tokens (u32 [batch]); returns ``ok``."""
+        ring, state, cap = self._common()
+        check(_lib.load().vpa_allocate_rows(
+            self.block_tables.data_ptr(), self.cols, self.row_blocks.data_ptr(),
+            target_tokens.contiguous().data_ptr(), self.ok.data_ptr(), ring, state, cap,
+            self.block_size, self.batch, _stream(self.block_tables)))
+        return self.ok
+
+    def step(self, finished: Optional[torch.Tensor] = None):
+        """One decode step: returns (slot_mapping, context_lens) device tensors."""
+        ring, state, cap = self._common()
+        check(_lib.load().vpa_decode_step_metadata(
+            self.block_tables.data_ptr(), self.cols, self.row_blocks.data_ptr(),
+            self.positions.data_ptr(), _ptr(finished), ring, state, cap, self.block_size,
+            self.slot_mapping.data_ptr(), self.context_lens.data_ptr(), self.status.data_ptr(),
+            self.batch, _stream(self.block_tables)))
+        return self.slot_mapping, self.context_lens
+
+    def release(self, keep_blocks: torch.Tensor) -> None:
+        """Rows keep their first keep_blocks[r] blocks (u32 [batch]), the rest go back."""
+        ring, state, cap = self._common()
+        check(_lib.load().vpa_release_blocks(
+            self.block_tables.data_ptr(), self.cols, self.row_blocks.data_ptr(),
+            keep_blocks.contiguous().data_ptr(), ring, state, cap, self.batch,
+            _stream(self.block_tables)))
+
