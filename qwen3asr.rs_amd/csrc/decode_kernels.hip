@@ -345,6 +345,9 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(
   }
 }
 
+#ifndef VPA_DECODE_FP8_NV
+#define VPA_DECODE_FP8_NV 8
+#endif
 #ifndef VPA_DECODE_ROWS_WAVES_PER_EU
 #define VPA_DECODE_ROWS_WAVES_PER_EU 3
 #endif
@@ -397,7 +400,7 @@ void paged_decode_rows_kernel(
   // over its 64 / BS lanes with DPP / permlane swaps. A V stage reads BKS
   // value tiles the same way (lane l: row l / (BS/8) + k * 64 / (BS/8),
   // tokens (l % (BS/8)) * 8 .. +7).
-  constexpr int NV = 8;                   // 16-byte loads per lane per stage
+  constexpr int NV = kF8 ? VPA_DECODE_FP8_NV : 8;  // 16-byte loads per lane per stage
   constexpr int KPL = D * BS / (X * 64);  // loads per lane per tile (K or V)
   constexpr int LPT = 64 / BS;            // lanes per token in a key tile
   constexpr int BKS = NV / KPL;           // tiles per stage
@@ -754,6 +757,13 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
 #endif
 constexpr int kRowsPT = VPA_DECODE_ROWS_PT;  // partition tokens per wave of the rows kernel
 constexpr int kRowsWaves = VPA_DECODE_ROWS_WAVES;  // waves (partitions) per workgroup
+// fp8 caches: the same chunk (the plan is shared) over fewer, longer waves,
+// so that each wave keeps as many bytes in flight as a 16-bit one
+#ifndef VPA_DECODE_FP8_WAVES
+#define VPA_DECODE_FP8_WAVES 2
+#endif
+constexpr int kF8Waves = VPA_DECODE_FP8_WAVES;
+constexpr int kF8PT = kRowsPT * kRowsWaves / kF8Waves;
 static_assert(kRowsPT >= kDecodeMinPartitionTokens, "workspace sized for 128-token partitions");
 
 // Merge of split-K partials: persistent waves over (sequence, query head)
@@ -825,7 +835,11 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
                                 int32_t max_ctx, float scale, int32_t num_seqs,
                                 int32_t num_heads, const CacheGeom& g, const DecodeWorkspace& ws,
                                 hipStream_t stream, const float* k_scale, const float* v_scale) {
-  constexpr int kChunk = kRowsPT * kRowsWaves;  // tokens per workgroup
+  constexpr bool kFp8 = std::is_same_v<C, fp8_t>;
+  constexpr int PT = kFp8 ? kF8PT : kRowsPT;
+  constexpr int NW = kFp8 ? kF8Waves : kRowsWaves;
+  constexpr int kChunk = PT * NW;  // tokens per workgroup (the same for every cache type)
+  static_assert(kChunk == kRowsPT * kRowsWaves, "one plan serves every cache type");
   const int cap_tokens = bts * g.block_size;
   hipError_t e = hipSuccess;
   if (!ws.planned) {
@@ -836,8 +850,8 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
   }
   const int max_chunks = max(1, (max_ctx + kChunk - 1) / kChunk);
   const int64_t units = (int64_t)num_seqs * max_chunks * g.num_kv_heads;
-  hipLaunchKernelGGL((paged_decode_rows_kernel<T, C, D, BS, G, kRowsPT, kRowsWaves>),
-                     dim3((unsigned)units), dim3(64 * kRowsWaves), 0, stream,
+  hipLaunchKernelGGL((paged_decode_rows_kernel<T, C, D, BS, G, PT, NW>),
+                     dim3((unsigned)units), dim3(64 * NW), 0, stream,
                      static_cast<T*>(out), static_cast<const T*>(q), static_cast<const C*>(kc),
                      static_cast<const C*>(vc), bt, bts, scale, num_heads, g.num_kv_heads,
                      g.num_blocks, g.block_stride, g.head_stride, ws.part_out, ws.max_parts,
