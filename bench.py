@@ -169,37 +169,54 @@ def timed_ms(fn, reps):
 
 def cpu_baseline(w, layers, budget_s):
     """Time the oracle's restatement of the reference CPU decode path on a
-    bounded sample: whole layers of the same workload (all sequences), copied
-    to host memory, as many layers as fit the time budget."""
+    bounded sample of the same workload: groups of up to 256 sequences of a
+    layer (c3: whole layers), in order, until the time budget is spent. Each
+    group's blocks are copied to host memory with its tables renumbered over
+    them (the c5 pool does not fit host memory)."""
     import numpy as np
+    import torch
 
     from oracle import oracle as orc
+    from vpa import workloads
 
     code = {"bf16": orc.BF16, "f16": orc.F16, "f32": orc.F32}[w.dtype]
 
     def host(t):
-        import torch
         t = t.detach().cpu().contiguous()
         if t.dtype == torch.float32:
             return t.numpy()
         return t.view(torch.int16).numpy().view(np.uint16)
 
     scale = w.head_dim ** -0.5
+    kvb = w.kv_bytes_per_token()
+    group = min(w.num_seqs, 256)
     done_bytes = 0
     elapsed = 0.0
-    layers_done = 0
+    seq_layers = 0
+    groups = 0
     threads = 1
     for i, L in enumerate(layers):
-        kc, vc = host(L["kc"]), host(L["vc"])
-        q, k, v = host(L["q"]), host(L["k"]), host(L["v"])
         meta = w.layers[i]
-        t0 = time.perf_counter()
-        _, threads = orc.cpu_baseline_decode_step(q, k, v, meta.slot_mapping, kc, vc,
-                                                  meta.block_tables, w.context_lens, scale,
-                                                  dtype=code)
-        elapsed += time.perf_counter() - t0
-        done_bytes += w.decode_bytes_per_layer() + w.append_bytes_per_layer()
-        layers_done += 1
+        for s0 in range(0, w.num_seqs, group):
+            sl = slice(s0, s0 + group)
+            lens = w.context_lens[sl]
+            blocks, bt, slots = workloads.compact_tables(meta.block_tables[sl], lens,
+                                                         w.block_size, meta.slot_mapping[sl])
+            idx = torch.from_numpy(blocks).to(L["kc"].device)
+            kc, vc = host(L["kc"].index_select(0, idx)), host(L["vc"].index_select(0, idx))
+            q, k, v = host(L["q"][sl]), host(L["k"][sl]), host(L["v"][sl])
+            t0 = time.perf_counter()
+            _, threads = orc.cpu_baseline_decode_step(q, k, v, slots, kc, vc, bt, lens, scale,
+                                                      dtype=code)
+            elapsed += time.perf_counter() - t0
+            n = lens.astype(np.int64)
+            done_bytes += int((n * kvb + 2 * w.num_heads * w.head_dim * w.elem_bytes
+                               + 4 * ((n + w.block_size - 1) // w.block_size) + 4
+                               + 2 * kvb + 8).sum())
+            seq_layers += len(n)
+            groups += 1
+            if elapsed >= budget_s:
+                break
         if elapsed >= budget_s:
             break
     gbps = done_bytes / elapsed / 1e9
@@ -208,9 +225,9 @@ def cpu_baseline(w, layers, budget_s):
         "unit": "GB/s",
         "cores": int(threads),
         "kind": "port",
-        "sample": (f"{layers_done} of {len(layers)} layers of {w.name} (all {w.num_seqs} "
-                   f"sequences, append + decode), {elapsed:.1f} s on {os.cpu_count()} visible "
-                   f"host CPUs"),
+        "sample": (f"{groups} group(s) of up to {group} sequences of one layer of {w.name} "
+                   f"({seq_layers} sequence-layers of {w.num_seqs} x {len(layers)}, append + "
+                   f"decode), {elapsed:.1f} s on {os.cpu_count()} visible host CPUs"),
     }
 
 

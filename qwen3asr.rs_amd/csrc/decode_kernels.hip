@@ -345,6 +345,9 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(
   }
 }
 
+#ifndef VPA_DECODE_MERGE_WAVES_PER_CU
+#define VPA_DECODE_MERGE_WAVES_PER_CU 16
+#endif
 #ifndef VPA_DECODE_FP8_NV
 #define VPA_DECODE_FP8_NV 8
 #endif
@@ -859,7 +862,8 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
   e = hipGetLastError();
   if (e != hipSuccess || max_chunks <= 1) return e;
   const int64_t munits = (int64_t)num_seqs * num_heads;
-  const int64_t mwaves = std::min<int64_t>(munits, (int64_t)device_cu_count() * 8);
+  const int64_t mwaves =
+      std::min<int64_t>(munits, (int64_t)device_cu_count() * VPA_DECODE_MERGE_WAVES_PER_CU);
   hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)mwaves), dim3(64), 0, stream,
                      static_cast<T*>(out), cl, num_seqs, max_ctx, cap_tokens, kChunk, num_heads,
                      ws.part_out, ws.max_parts);

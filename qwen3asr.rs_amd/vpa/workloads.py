@@ -122,6 +122,35 @@ def _slots(bt: np.ndarray, lens: np.ndarray, bs: int) -> np.ndarray:
     return blk * bs + pos % bs
 
 
+def compact_tables(block_tables: np.ndarray, lens: np.ndarray, bs: int,
+                   slots: np.ndarray | None = None):
+    """The blocks a set of sequences reads and their tables renumbered over
+    those blocks alone, so that a sample of a pool too large for host memory
+    (c5) can be copied out and handed to a CPU restatement.
+
+    Returns (blocks, tables, slots): `blocks` is the sorted int64 array of
+    physical ids read, block 0 (the null block) always first; `tables[i, c]`
+    is the index into `blocks` of block_tables[i, c] for the columns a
+    context of lens[i] tokens uses (0 elsewhere); `slots`, when given, is
+    renumbered the same way (PAD -1 kept)."""
+    lens = np.asarray(lens, dtype=np.int64)
+    need = (lens + bs - 1) // bs
+    used = [block_tables[i, :n].astype(np.int64) for i, n in enumerate(need)]
+    blocks = np.unique(np.concatenate([np.zeros(1, np.int64)] + used))
+    tables = np.zeros((len(lens), max(int(need.max()) if len(need) else 1, 1)), np.uint32)
+    for i, ids in enumerate(used):
+        tables[i, :len(ids)] = np.searchsorted(blocks, ids)
+    new_slots = None
+    if slots is not None:
+        slots = np.asarray(slots, dtype=np.int64)
+        blk = slots // bs
+        idx = np.searchsorted(blocks, np.where(slots >= 0, blk, 0))
+        if np.any((slots >= 0) & (blocks[np.minimum(idx, len(blocks) - 1)] != blk)):
+            raise ValueError("a slot lies in a block the tables do not read")
+        new_slots = np.where(slots >= 0, idx * bs + slots % bs, -1)
+    return blocks, tables, new_slots
+
+
 def c1(seed: int = 1) -> DecodeWorkload:
     """f32, B=1, L=512 (511 prefilled + 1 appended), 32 blocks taken from a
     seeded permutation of a 64-block pool, one layer."""
