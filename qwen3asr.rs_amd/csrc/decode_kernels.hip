@@ -305,42 +305,97 @@ __device__ __forceinline__ int clamp_context(uint32_t ctx, int max_ctx, int cap)
   return min((int)min(ctx, (uint32_t)max_ctx), cap);
 }
 
+// Item order. With 16-bit caches items stay in sequence order: long and
+// short chunks interleave over the whole launch, and the short ones, whose
+// waves are latency-bound, overlap the streaming of the long ones (grouping
+// them measured slower). With fp8 caches (two long waves per workgroup)
+// items are emitted longest first, a counting sort over kPlanMaxBuckets
+// classes of chunk length, stable within a class: measured 9 % faster.
+constexpr int kPlanMaxBuckets = 8;
+
+__host__ __device__ constexpr int plan_buckets(bool fp8_cache) {
+  return fp8_cache ? kPlanMaxBuckets : 1;
+}
+
+__device__ __forceinline__ int plan_bucket(int L, int p, int part_tokens, int buckets) {
+  if (L <= 0) return buckets - 1;
+  const int n = min(part_tokens, L - p * part_tokens);  // tokens of chunk p, >= 1
+  return (int)(((int64_t)(part_tokens - n) * buckets) / part_tokens);
+}
+
 __global__ __launch_bounds__(1024) void decode_plan_kernel(
     const uint32_t* __restrict__ context_lens, int32_t num_seqs, int32_t max_ctx,
-    int32_t cap_tokens, int32_t part_tokens, uint2* __restrict__ items,
+    int32_t cap_tokens, int32_t part_tokens, int32_t buckets, uint2* __restrict__ items,
     uint32_t* __restrict__ multi, uint32_t* __restrict__ queue) {
-  __shared__ uint32_t s_sum[1024];
+  constexpr int NB = kPlanMaxBuckets;
+  __shared__ uint32_t s_wave[16][NB];
+  __shared__ uint32_t s_base[NB + 1];
   __shared__ uint32_t s_multi;
   if (threadIdx.x == 0) s_multi = 0;
   const int tid = threadIdx.x;
-  const int chunk = (num_seqs + 1023) / 1024;
-  const int s0 = min(tid * chunk, num_seqs);
-  const int s1 = min(s0 + chunk, num_seqs);
-  uint32_t local = 0;
-  for (int s = s0; s < s1; ++s) {
-    const int L = clamp_context(context_lens[s], max_ctx, cap_tokens);
-    local += L > 0 ? (uint32_t)((L + part_tokens - 1) / part_tokens) : 1u;
-  }
-  s_sum[tid] = local;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const uint32_t v = tid >= off ? s_sum[tid - off] : 0u;
-    __syncthreads();
-    s_sum[tid] += v;
-    __syncthreads();
-  }
-  uint32_t pos = s_sum[tid] - local;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int per = (num_seqs + 1023) / 1024;
+  const int s0 = min(tid * per, num_seqs);
+  const int s1 = min(s0 + per, num_seqs);
+  uint32_t cnt[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) cnt[b] = 0;
   for (int s = s0; s < s1; ++s) {
     const int L = clamp_context(context_lens[s], max_ctx, cap_tokens);
     const int n = L > 0 ? (L + part_tokens - 1) / part_tokens : 1;
-    for (int p = 0; p < n; ++p)
-      items[pos++] = make_uint2(((uint32_t)s << 16) | (uint32_t)p, (uint32_t)max(L, 0));
+    for (int p = 0; p < n; ++p) {
+      const int b = plan_bucket(L, p, part_tokens, buckets);
+#pragma unroll
+      for (int c = 0; c < NB; ++c) cnt[c] += c == b;
+    }
+  }
+  // per bucket: exclusive prefix over the threads (wave scan, then waves)
+  uint32_t pre[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    uint32_t x = cnt[b];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    pre[b] = x - cnt[b];
+    if (lane == 63) s_wave[wave][b] = x;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t acc = 0;
+    for (int b = 0; b < NB; ++b) {
+      s_base[b] = acc;
+      for (int w = 0; w < 16; ++w) {
+        const uint32_t t = s_wave[w][b];
+        s_wave[w][b] = acc;
+        acc += t;
+      }
+    }
+    s_base[NB] = acc;
+  }
+  __syncthreads();
+  uint32_t pos[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) pos[b] = s_wave[wave][b] + pre[b];
+  for (int s = s0; s < s1; ++s) {
+    const int L = clamp_context(context_lens[s], max_ctx, cap_tokens);
+    const int n = L > 0 ? (L + part_tokens - 1) / part_tokens : 1;
+    for (int p = 0; p < n; ++p) {
+      const int b = plan_bucket(L, p, part_tokens, buckets);
+      uint32_t at = 0;
+#pragma unroll
+      for (int c = 0; c < NB; ++c)
+        if (c == b) at = pos[c]++;
+      items[at] = make_uint2(((uint32_t)s << 16) | (uint32_t)p, (uint32_t)max(L, 0));
+    }
     if (n > 1) multi[atomicAdd(&s_multi, 1u)] = (uint32_t)s;
   }
   __syncthreads();
-  if (tid == 1023) {
+  if (tid == 0) {
     queue[0] = 0u;
-    queue[1] = s_sum[1023];
+    queue[1] = s_base[NB];
     queue[2] = s_multi;
   }
 }
@@ -847,7 +902,8 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
   hipError_t e = hipSuccess;
   if (!ws.planned) {
     hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, cl, num_seqs,
-                       max_ctx, cap_tokens, kChunk, ws.items, ws.multi, ws.queue);
+                       max_ctx, cap_tokens, kChunk, plan_buckets(kFp8), ws.items, ws.multi,
+                       ws.queue);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -977,14 +1033,16 @@ hipError_t dispatch_decode(int dtype, int D, int BS, int group, A... args) {
 
 }  // namespace
 
-hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t max_context_len,
-                              int32_t block_table_stride, int32_t num_seqs, const CacheGeom& g,
-                              const DecodeWorkspace& ws, hipStream_t stream) {
+hipError_t launch_decode_plan(int dtype, int cache_dtype, const uint32_t* context_lens,
+                              int32_t max_context_len, int32_t block_table_stride,
+                              int32_t num_seqs, const CacheGeom& g, const DecodeWorkspace& ws,
+                              hipStream_t stream) {
   const bool rows = (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) && g.head_dim <= 128;
   if (!rows || num_seqs == 0) return hipSuccess;
   hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, context_lens, num_seqs,
                      max_context_len, block_table_stride * g.block_size, kRowsPT * kRowsWaves,
-                     ws.items, ws.multi, ws.queue);
+                     plan_buckets(cache_dtype == VPA_DTYPE_FP8_E4M3), ws.items, ws.multi,
+                     ws.queue);
   return hipGetLastError();
 }
 
