@@ -291,8 +291,9 @@ def decode_fp8(w, dev, reps):
 def prefill_c4(dev, reps=10):
     """Row a3 measured alongside the headline: c4 (64 sequences x 512 new
     tokens over 0..1024 prior tokens, bf16) append with reshape_and_cache,
-    then causal chunked-prefill attention over the paged cache; HIP events
-    around each op on the current stream, after 2 untimed calls."""
+    then causal chunked-prefill attention over the paged cache, and the same
+    prefill over fp8 caches; HIP events around each op on the current
+    stream, after 2 untimed calls."""
     import numpy as np
     import torch
 
@@ -325,8 +326,25 @@ def prefill_c4(dev, reps=10):
                                            causal=True, max_query_len=mq, max_context_len=mk,
                                            out=out)
 
+    # the same prefill over fp8 (E4M3FN) caches, scales 1
+    one = torch.ones(1, dtype=torch.float32, device=dev)
+
+    def fp8_cache(shape):
+        b = torch.randint(0, 256, shape, generator=g, device=dev, dtype=torch.uint8)
+        b[(b & 0x7F) == 0x7F] = 0x38  # no NaN codes
+        return b.view(torch.float8_e4m3fn)
+
+    kc8 = fp8_cache((w.num_blocks, kvh, d // 16, bs, 16))
+    vc8 = fp8_cache((w.num_blocks, kvh, d, bs))
+    out8 = torch.empty_like(q)
+
+    def prefill_fp8():
+        vpa.paged_attention_varlen_prefill(q, kc8, vc8, bt, cl, cu, one, one, d ** -0.5, 1.0,
+                                           causal=True, max_query_len=mq, max_context_len=mk,
+                                           out=out8)
+
     res = {}
-    for name, fn in (("append", append), ("prefill", prefill)):
+    for name, fn in (("append", append), ("prefill", prefill), ("prefill_fp8", prefill_fp8)):
         for _ in range(2):
             fn()
         e0 = torch.cuda.Event(enable_timing=True)
@@ -348,6 +366,8 @@ def prefill_c4(dev, reps=10):
         "append_frac_of_peak": round(app_bytes / (res["append"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
         "prefill_us": round(res["prefill"], 2),
         "prefill_tflops": round(tflops, 2),
+        "prefill_fp8_cache_us": round(res["prefill_fp8"], 2),
+        "prefill_fp8_cache_tflops": round(flops / (res["prefill_fp8"] * 1e-6) / 1e12, 2),
         "roofline": {"kernel": "chunked_prefill_paged_attention", "bound": "mfma",
                      "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),

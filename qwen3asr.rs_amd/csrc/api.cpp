@@ -467,15 +467,16 @@ int vpa_chunked_prefill_paged_attention(
     float softmax_scale, int32_t causal, int32_t num_heads, int32_t num_kv_heads,
     int32_t head_dim, int32_t block_size, int64_t num_blocks, int64_t cache_block_stride,
     int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype, void* stream) {
-  (void)k_scale;
-  (void)v_scale;
   clear_error();
   const char* op = "chunked_prefill_paged_attention";
-  if (dtype != cache_dtype)
+  const bool fp8 = cache_dtype == VPA_DTYPE_FP8_E4M3;
+  if (dtype != cache_dtype && !(fp8 && (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16)))
     return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from query dtype %s", op,
                 dtype_name(cache_dtype), dtype_name(dtype));
   int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
                        cache_block_stride, cache_head_stride, key_cache, value_cache);
+  if (rc != VPA_OK) return rc;
+  rc = check_scales(op, cache_dtype, k_scale, v_scale);
   if (rc != VPA_OK) return rc;
   if (num_seqs < 0 || num_heads <= 0 || max_query_len < 0 || max_kv_len < 0 ||
       total_query_rows < 0 || block_table_stride < 0)
@@ -488,11 +489,12 @@ int vpa_chunked_prefill_paged_attention(
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: num_heads=%d not a multiple of num_kv_heads=%d",
                 op, num_heads, num_kv_heads);
   const int group = num_heads / num_kv_heads;
-  if (!prefill_supported(dtype, head_dim, block_size, group))
+  if (!prefill_supported(dtype, cache_dtype, head_dim, block_size, group))
     return fail(VPA_ERR_UNSUPPORTED,
-                "%s: no MFMA kernel for dtype=%s head_dim=%d block_size=%d group=%d (bf16/f16, "
-                "head_dim 64/128, block_size 8/16/32, 1/2/4 query heads per kv head)",
-                op, dtype_name(dtype), head_dim, block_size, group);
+                "%s: no MFMA kernel for dtype=%s cache=%s head_dim=%d block_size=%d group=%d "
+                "(bf16/f16, head_dim 64/128, block_size 8/16/32, 1/2/4 query heads per kv "
+                "head; fp8 caches: head_dim 128, block_size 16/32)",
+                op, dtype_name(dtype), dtype_name(cache_dtype), head_dim, block_size, group);
   if (num_seqs == 0 || max_query_len == 0 || total_query_rows == 0) return VPA_OK;
   {
     const int ppb = prefill_positions_per_workgroup(group);
@@ -515,11 +517,13 @@ int vpa_chunked_prefill_paged_attention(
                 block_table_stride, max_kv_len, block_size);
   CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
               cache_head_stride};
-  return hip_status(op, launch_prefill_paged(dtype, out, query, key_cache, value_cache,
-                                             block_tables, block_table_stride, cu_seqlens_q,
-                                             context_lens, num_seqs, max_query_len, max_kv_len,
-                                             total_query_rows, softmax_scale, causal, num_heads,
-                                             g, static_cast<hipStream_t>(stream)));
+  return hip_status(op, launch_prefill_paged(dtype, cache_dtype, out, query, key_cache,
+                                             value_cache, block_tables, block_table_stride,
+                                             cu_seqlens_q, context_lens, num_seqs, max_query_len,
+                                             max_kv_len, total_query_rows, softmax_scale, causal,
+                                             num_heads, g, fp8 ? k_scale : nullptr,
+                                             fp8 ? v_scale : nullptr,
+                                             static_cast<hipStream_t>(stream)));
 }
 
 int vpa_argmax_rows(const void* logits, int64_t row_stride, int32_t vocab, int32_t num_rows,

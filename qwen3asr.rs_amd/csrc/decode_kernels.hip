@@ -474,8 +474,14 @@ void paged_decode_rows_kernel(
   const uint32_t w = blockIdx.x;
   const int j = (int)(w % (uint32_t)num_kv_heads);
   const uint32_t want = w / (uint32_t)num_kv_heads;  // index of this workgroup's item
-  if (want >= queue[1]) return;  // surplus workgroup of the grid
+  // the list holds num_seqs * ceil(max_ctx / 128) >= gridDim.x / num_kv_heads
+  // entries, so the item is read together with the count (one round trip)
+  const uint32_t nitems = queue[1];
   const uint2 item = items[want];
+  // (the empty asm keeps the compiler from sinking the item load below the
+  // count test)
+  asm volatile("" ::"s"(nitems), "s"(item.x), "s"(item.y));
+  if (want >= nitems) return;  // surplus workgroup of the grid
   const int s = (int)(item.x >> 16);
   const int chunk = (int)(item.x & 0xffffu);
   // a work list built by an earlier call is only trusted within this call's

@@ -130,6 +130,33 @@ __device__ __forceinline__ v4i_t lds_read_b128(uint32_t addr) {
   return r;
 }
 
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+template <int OFF>
+__device__ __forceinline__ v2i_t lds_read_b64(uint32_t addr) {
+  v2i_t r;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int STRIDE, int... I>
+__device__ __forceinline__ void lds_read_seq8(v2i_t* dst, uint32_t addr,
+                                              std::integer_sequence<int, I...>) {
+  ((dst[I] = lds_read_b64<I * STRIDE>(addr)), ...);
+}
+template <int STRIDE, int SECOND, int... I>
+__device__ __forceinline__ void lds_read_pairs8(v2i_t (*dst)[2], uint32_t addr,
+                                                std::integer_sequence<int, I...>) {
+  ((dst[I][0] = lds_read_b64<I * STRIDE>(addr),
+    dst[I][1] = lds_read_b64<I * STRIDE + SECOND>(addr)),
+   ...);
+}
+// Eight E4M3FN bytes -> eight values of T (exact), as one MFMA operand.
+template <typename T>
+__device__ __forceinline__ v4i_t fp8x8_operand(const v2i_t& b) {
+  const uint32_t lo = (uint32_t)b[0], hi = (uint32_t)b[1];
+  return v4i_t{(int)fp8x2_to_pk<T>(lo, false), (int)fp8x2_to_pk<T>(lo, true),
+               (int)fp8x2_to_pk<T>(hi, false), (int)fp8x2_to_pk<T>(hi, true)};
+}
+
 // dst[i] = 16 bytes at addr + i * STRIDE (+ SECOND for dst2), i < N
 template <int STRIDE, int... I>
 __device__ __forceinline__ void lds_read_seq(v4i_t* dst, uint32_t addr,
@@ -166,19 +193,22 @@ __device__ __forceinline__ constexpr int tile_key_of_row(int i) {
   return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
 }
 
-template <typename T, int D, int BS, int G>
+template <typename T, typename C, int D, int BS, int G>
 __global__ __launch_bounds__(kPrefillThreads)
 __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_paged_kernel(
-    T* __restrict__ out, const T* __restrict__ query, const T* __restrict__ key_cache,
-    const T* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
+    T* __restrict__ out, const T* __restrict__ query, const C* __restrict__ key_cache,
+    const C* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
     int32_t block_table_stride, const uint32_t* __restrict__ cu_seqlens_q,
     const uint32_t* __restrict__ context_lens, int32_t num_seqs, int32_t max_query_len,
     int32_t max_kv_len, int64_t total_query_rows, float scale_log2, int32_t causal,
     int32_t num_heads, int32_t num_kv_heads, int64_t num_blocks, int64_t block_stride,
-    int64_t head_stride, int32_t q_tiles) {
+    int64_t head_stride, int32_t q_tiles, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale) {
+  constexpr bool kF8 = std::is_same_v<C, fp8_t>;
+  static_assert(kF8 || std::is_same_v<C, T>, "cache type is the query type or fp8");
   constexpr int KT = kPrefillKeys;
   constexpr int NS = kPrefillStages;
-  constexpr int X = 8;          // 16-bit elements per 16-byte vector
+  constexpr int X = kF8 ? 16 : 8;  // cache elements per 16-byte unit
   constexpr int PPW = 32 / G;   // query positions per wave
   constexpr int PPB = 4 * PPW;  // query positions per workgroup
   constexpr int KS = D / 16;    // k-steps of Q.K^T
@@ -241,6 +271,13 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
       wave_end <= wpos0 ? 0 : max(0, causal ? min(k_len, wave_end + shift) : k_len);
   const int wave_min_limit = causal ? wpos0 + shift : k_len - 1;
 
+  // fp8: k_scale folds into the softmax scale (its sign too), v_scale into
+  // the output
+  float vs = 1.f;
+  if constexpr (kF8) {
+    scale_log2 *= *k_scale;
+    vs = *v_scale;
+  }
   uint4 qop[KS];
   {
     const T* qrow = query + (row * num_heads + head) * D + 8 * half;
@@ -269,8 +306,8 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   float m = -INFINITY;  // running max of the row, log2 units
   float lsum = 0.f;     // this lane's share of the row's exp sum
 
-  const T* kbase = key_cache + (int64_t)j * head_stride;
-  const T* vbase = value_cache + (int64_t)j * head_stride;
+  const C* kbase = key_cache + (int64_t)j * head_stride;
+  const C* vbase = value_cache + (int64_t)j * head_stride;
   const uint32_t* bt = block_tables + (int64_t)s * block_table_stride;
   const int last_blk = max(k_len - 1, 0) / BS;
 
@@ -327,15 +364,22 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   };
 
   // LDS byte offsets of this lane's operand reads within a stage
+  // (16-bit: chunk 2 ks + half of the key, one unit; fp8: bytes 8 half ..
+  // 8 half + 7 of chunk ks)
   const uint32_t ka_lane = [&] {
     const int key = tile_key_of_row(col);
-    return (uint32_t)(((key / BS) * RBK + half * BS + key % BS) * 16);
+    if constexpr (kF8) return (uint32_t)(((key / BS) * RBK + key % BS) * 16 + 8 * half);
+    else return (uint32_t)(((key / BS) * RBK + half * BS + key % BS) * 16);
   }();
   // unit group g = 2 k2 + half of the tile (keys 8g .. 8g+7) sits at
   // (g / UB) * RBV + (g % UB) * D units; that splits into a k2 and a half term
+  // (fp8: units hold 16 keys; keys 8g .. 8g+7 are bytes 8 (g % 2) .. of
+  // unit g / 2)
   auto vgroup = [](int g) { return (g / UB) * RBV + (g % UB) * D; };
-  constexpr int kVStep1 = ((2 / UB) * RBV + (2 % UB) * D) * 16;
-  const uint32_t va_lane = (uint32_t)((vgroup(half) + col) * 16);
+  constexpr int kVStep1 = kF8 ? ((1 / UB) * RBV + (1 % UB) * D) * 16
+                              : ((2 / UB) * RBV + (2 % UB) * D) * 16;
+  const uint32_t va_lane =
+      kF8 ? (uint32_t)(col * 16 + 8 * half) : (uint32_t)((vgroup(half) + col) * 16);
 
   // keys of tile t that exist: inside the context and in a present block
   // (uniform over the workgroup)
@@ -355,13 +399,14 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
 
   // Zero the LDS values of the keys vmask leaves out: their slots hold
   // stale data (maybe NaN), and a zero probability times NaN would poison O.
-  // Element k % 8 of unit (k / 8, d) holds key k of dim d.
+  // Element k % X of unit (k / X, d) holds key k of dim d.
   auto zero_absent_values = [&](auto sc, uint32_t vmask) {
-    uint16_t* v16 = reinterpret_cast<uint16_t*>(vst(sc));
+    using E = std::conditional_t<kF8, uint8_t, uint16_t>;
+    E* ve = reinterpret_cast<E*>(vst(sc));
     const uint32_t absent = ~vmask;
     for (int e = tid; e < KT * D; e += kPrefillThreads) {
       const int k = e / D, d = e % D;
-      if ((absent >> k) & 1u) v16[(vgroup(k / 8) + d) * X + k % 8] = 0;
+      if ((absent >> k) & 1u) ve[(vgroup(k / X) + d) * X + k % X] = 0;
     }
   };
 
@@ -375,12 +420,23 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     // S^T = K . Q^T; the K operand of k-step ks is chunk 2 ks + half of the
     // key in row col
     v4i_t kop[KS];
-    lds_read_seq<2 * BS * 16>(kop, ka_lane + lds_addr(sk), std::make_integer_sequence<int, KS>{});
-    if constexpr (KS == 8) {
+    if constexpr (kF8) {
+      static_assert(KS == 8, "fp8: head_dim 128");
+      v2i_t k8[KS];
+      lds_read_seq8<BS * 16>(k8, ka_lane + lds_addr(sk), std::make_integer_sequence<int, KS>{});
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k8[0]), "+v"(k8[1]), "+v"(k8[2]), "+v"(k8[3]),
+                   "+v"(k8[4]), "+v"(k8[5]), "+v"(k8[6]), "+v"(k8[7]));
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kop[ks] = fp8x8_operand<T>(k8[ks]);
+    } else if constexpr (KS == 8) {
+      lds_read_seq<2 * BS * 16>(kop, ka_lane + lds_addr(sk),
+                                std::make_integer_sequence<int, KS>{});
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kop[0]), "+v"(kop[1]), "+v"(kop[2]),
                    "+v"(kop[3]), "+v"(kop[4]), "+v"(kop[5]), "+v"(kop[6]), "+v"(kop[7]));
     } else {
       static_assert(KS == 4, "head_dim 64 or 128");
+      lds_read_seq<2 * BS * 16>(kop, ka_lane + lds_addr(sk),
+                                std::make_integer_sequence<int, KS>{});
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kop[0]), "+v"(kop[1]), "+v"(kop[2]),
                    "+v"(kop[3]));
     }
@@ -434,13 +490,27 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     // 16 k2 + 8h + 7, one unit of row d = 32 dt + col (values of absent keys
     // were zeroed in LDS by the step)
     v4i_t vop[DT][2];
-    lds_read_pairs<32 * 16, kVStep1>(vop, va_lane + lds_addr(sv), std::make_integer_sequence<int, DT>{});
-    if constexpr (DT == 4) {
+    if constexpr (kF8) {
+      v2i_t v8[DT][2];
+      lds_read_pairs8<32 * 16, kVStep1>(v8, va_lane + lds_addr(sv),
+                                        std::make_integer_sequence<int, DT>{});
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(v8[0][0]), "+v"(v8[0][1]), "+v"(v8[1][0]), "+v"(v8[1][1]),
+                     "+v"(v8[2][0]), "+v"(v8[2][1]), "+v"(v8[3][0]), "+v"(v8[3][1]));
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) vop[dt][k2] = fp8x8_operand<T>(v8[dt][k2]);
+    } else if constexpr (DT == 4) {
+      lds_read_pairs<32 * 16, kVStep1>(vop, va_lane + lds_addr(sv),
+                                       std::make_integer_sequence<int, DT>{});
       asm volatile("s_waitcnt lgkmcnt(0)"
                    : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[1][0]), "+v"(vop[1][1]),
                      "+v"(vop[2][0]), "+v"(vop[2][1]), "+v"(vop[3][0]), "+v"(vop[3][1]));
     } else {
       static_assert(DT == 2, "head_dim 64 or 128");
+      lds_read_pairs<32 * 16, kVStep1>(vop, va_lane + lds_addr(sv),
+                                       std::make_integer_sequence<int, DT>{});
       asm volatile("s_waitcnt lgkmcnt(0)"
                    : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[1][0]), "+v"(vop[1][1]));
     }
@@ -490,7 +560,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   }
 
   const float total = sum_xor32(lsum);
-  const float inv = total > 0.f ? 1.f / total : 0.f;  // a row that sees no key gives 0
+  const float inv = total > 0.f ? vs / total : 0.f;  // a row that sees no key gives 0
   if (row_ok) {
     T* orow = out + (row * num_heads + head) * D;
 #pragma unroll
@@ -505,128 +575,112 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   }
 }
 
-template <typename T, int D, int BS, int G>
-hipError_t launch_prefill_t(void* out, const void* query, const void* key_cache,
-                            const void* value_cache, const uint32_t* block_tables,
-                            int32_t block_table_stride, const uint32_t* cu_seqlens_q,
-                            const uint32_t* context_lens, int32_t num_seqs,
-                            int32_t max_query_len, int32_t max_kv_len, int64_t total_query_rows,
-                            float scale, int32_t causal, int32_t num_heads, const CacheGeom& g,
-                            hipStream_t stream) {
+// Arguments after the template dispatch, shared by every instance.
+struct PrefillArgs {
+  void* out;
+  const void* query;
+  const void* key_cache;
+  const void* value_cache;
+  const uint32_t* block_tables;
+  int32_t block_table_stride;
+  const uint32_t* cu_seqlens_q;
+  const uint32_t* context_lens;
+  int32_t num_seqs, max_query_len, max_kv_len;
+  int64_t total_query_rows;
+  float scale;
+  int32_t causal, num_heads;
+  const float* k_scale;
+  const float* v_scale;
+};
+
+template <typename T, typename C, int D, int BS, int G>
+hipError_t launch_prefill_t(const PrefillArgs& a, const CacheGeom& g, hipStream_t stream) {
   constexpr int kPositions = 4 * 32 / G;
-  const int q_tiles = (max_query_len + kPositions - 1) / kPositions;
-  const int64_t grid = (int64_t)num_seqs * q_tiles * g.num_kv_heads;
+  const int q_tiles = (a.max_query_len + kPositions - 1) / kPositions;
+  const int64_t grid = (int64_t)a.num_seqs * q_tiles * g.num_kv_heads;
   if (grid == 0) return hipSuccess;
-  const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL((prefill_paged_kernel<T, D, BS, G>), dim3((uint32_t)grid),
-                     dim3(kPrefillThreads), 0, stream, static_cast<T*>(out),
-                     static_cast<const T*>(query), static_cast<const T*>(key_cache),
-                     static_cast<const T*>(value_cache), block_tables, block_table_stride,
-                     cu_seqlens_q, context_lens, num_seqs, max_query_len, max_kv_len,
-                     total_query_rows, scale_log2, causal, num_heads, g.num_kv_heads,
-                     g.num_blocks, g.block_stride, g.head_stride, q_tiles);
+  const float scale_log2 = a.scale * 1.4426950408889634f;
+  hipLaunchKernelGGL((prefill_paged_kernel<T, C, D, BS, G>), dim3((uint32_t)grid),
+                     dim3(kPrefillThreads), 0, stream, static_cast<T*>(a.out),
+                     static_cast<const T*>(a.query), static_cast<const C*>(a.key_cache),
+                     static_cast<const C*>(a.value_cache), a.block_tables, a.block_table_stride,
+                     a.cu_seqlens_q, a.context_lens, a.num_seqs, a.max_query_len, a.max_kv_len,
+                     a.total_query_rows, scale_log2, a.causal, a.num_heads, g.num_kv_heads,
+                     g.num_blocks, g.block_stride, g.head_stride, q_tiles, a.k_scale,
+                     a.v_scale);
   return hipGetLastError();
 }
 
-template <typename T, int D, int BS>
-hipError_t dispatch_group(int group, void* out, const void* query, const void* key_cache,
-                          const void* value_cache, const uint32_t* block_tables,
-                          int32_t block_table_stride, const uint32_t* cu_seqlens_q,
-                          const uint32_t* context_lens, int32_t num_seqs, int32_t max_query_len,
-                          int32_t max_kv_len, int64_t total_query_rows, float scale,
-                          int32_t causal, int32_t num_heads, const CacheGeom& g,
+template <typename T, typename C, int D, int BS>
+hipError_t dispatch_group(int group, const PrefillArgs& a, const CacheGeom& g,
                           hipStream_t stream) {
-#define VPA_PREFILL_G(GG)                                                                       \
-  case GG:                                                                                      \
-    return launch_prefill_t<T, D, BS, GG>(out, query, key_cache, value_cache, block_tables,    \
-                                          block_table_stride, cu_seqlens_q, context_lens,     \
-                                          num_seqs, max_query_len, max_kv_len,                 \
-                                          total_query_rows, scale, causal, num_heads, g, stream);
   switch (group) {
-    VPA_PREFILL_G(1)
-    VPA_PREFILL_G(2)
-    VPA_PREFILL_G(4)
+    case 1:
+      return launch_prefill_t<T, C, D, BS, 1>(a, g, stream);
+    case 2:
+      return launch_prefill_t<T, C, D, BS, 2>(a, g, stream);
+    case 4:
+      return launch_prefill_t<T, C, D, BS, 4>(a, g, stream);
     default:
       return hipErrorInvalidValue;
   }
-#undef VPA_PREFILL_G
 }
 
-template <typename T, int D>
-hipError_t dispatch_bs(int group, void* out, const void* query, const void* key_cache,
-                       const void* value_cache, const uint32_t* block_tables,
-                       int32_t block_table_stride, const uint32_t* cu_seqlens_q,
-                       const uint32_t* context_lens, int32_t num_seqs, int32_t max_query_len,
-                       int32_t max_kv_len, int64_t total_query_rows, float scale, int32_t causal,
-                       int32_t num_heads, const CacheGeom& g, hipStream_t stream) {
-#define VPA_PREFILL_BS(B)                                                                      \
-  case B:                                                                                      \
-    return dispatch_group<T, D, B>(group, out, query, key_cache, value_cache, block_tables,   \
-                                   block_table_stride, cu_seqlens_q, context_lens, num_seqs, \
-                                   max_query_len, max_kv_len, total_query_rows, scale, causal,\
-                                   num_heads, g, stream);
-  switch (g.block_size) {
-    VPA_PREFILL_BS(8)
-    VPA_PREFILL_BS(16)
-    VPA_PREFILL_BS(32)
-    default:
-      return hipErrorInvalidValue;
+// fp8 caches: head_dim 128, block_size 16 or 32 (a 32-key tile is then 256
+// 16-byte units, one DMA per lane of the workgroup)
+template <typename T, typename C>
+hipError_t dispatch_shape(int group, const PrefillArgs& a, const CacheGeom& g,
+                          hipStream_t stream) {
+  constexpr bool kF8 = std::is_same_v<C, fp8_t>;
+  if (g.head_dim == 128) {
+    if (g.block_size == 16) return dispatch_group<T, C, 128, 16>(group, a, g, stream);
+    if (g.block_size == 32) return dispatch_group<T, C, 128, 32>(group, a, g, stream);
+    if constexpr (!kF8)
+      if (g.block_size == 8) return dispatch_group<T, C, 128, 8>(group, a, g, stream);
   }
-#undef VPA_PREFILL_BS
-}
-
-template <typename T>
-hipError_t dispatch_dim(int group, void* out, const void* query, const void* key_cache,
-                        const void* value_cache, const uint32_t* block_tables,
-                        int32_t block_table_stride, const uint32_t* cu_seqlens_q,
-                        const uint32_t* context_lens, int32_t num_seqs, int32_t max_query_len,
-                        int32_t max_kv_len, int64_t total_query_rows, float scale, int32_t causal,
-                        int32_t num_heads, const CacheGeom& g, hipStream_t stream) {
-  switch (g.head_dim) {
-    case 64:
-      return dispatch_bs<T, 64>(group, out, query, key_cache, value_cache, block_tables,
-                                block_table_stride, cu_seqlens_q, context_lens, num_seqs,
-                                max_query_len, max_kv_len, total_query_rows, scale, causal,
-                                num_heads, g, stream);
-    case 128:
-      return dispatch_bs<T, 128>(group, out, query, key_cache, value_cache, block_tables,
-                                 block_table_stride, cu_seqlens_q, context_lens, num_seqs,
-                                 max_query_len, max_kv_len, total_query_rows, scale, causal,
-                                 num_heads, g, stream);
-    default:
-      return hipErrorInvalidValue;
+  if constexpr (!kF8) {
+    if (g.head_dim == 64) {
+      if (g.block_size == 8) return dispatch_group<T, C, 64, 8>(group, a, g, stream);
+      if (g.block_size == 16) return dispatch_group<T, C, 64, 16>(group, a, g, stream);
+      if (g.block_size == 32) return dispatch_group<T, C, 64, 32>(group, a, g, stream);
+    }
   }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-bool prefill_supported(int dtype, int head_dim, int block_size, int group) {
-  return (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) &&
-         (head_dim == 64 || head_dim == 128) &&
-         (block_size == 8 || block_size == 16 || block_size == 32) &&
-         (group == 1 || group == 2 || group == 4);
+bool prefill_supported(int dtype, int cache_dtype, int head_dim, int block_size, int group) {
+  if (!(dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) || !(group == 1 || group == 2 ||
+                                                                group == 4))
+    return false;
+  if (cache_dtype == VPA_DTYPE_FP8_E4M3) return head_dim == 128 && (block_size == 16 || block_size == 32);
+  return cache_dtype == dtype && (head_dim == 64 || head_dim == 128) &&
+         (block_size == 8 || block_size == 16 || block_size == 32);
 }
 
 int prefill_positions_per_workgroup(int group) { return 4 * 32 / group; }
 
-hipError_t launch_prefill_paged(int dtype, void* out, const void* query, const void* key_cache,
-                                const void* value_cache, const uint32_t* block_tables,
-                                int32_t block_table_stride, const uint32_t* cu_seqlens_q,
-                                const uint32_t* context_lens, int32_t num_seqs,
-                                int32_t max_query_len, int32_t max_kv_len,
+hipError_t launch_prefill_paged(int dtype, int cache_dtype, void* out, const void* query,
+                                const void* key_cache, const void* value_cache,
+                                const uint32_t* block_tables, int32_t block_table_stride,
+                                const uint32_t* cu_seqlens_q, const uint32_t* context_lens,
+                                int32_t num_seqs, int32_t max_query_len, int32_t max_kv_len,
                                 int64_t total_query_rows, float scale, int32_t causal,
-                                int32_t num_heads, const CacheGeom& g, hipStream_t stream) {
+                                int32_t num_heads, const CacheGeom& g, const float* k_scale,
+                                const float* v_scale, hipStream_t stream) {
   const int group = num_heads / g.num_kv_heads;
+  const PrefillArgs a{out,       query,        key_cache,      value_cache,  block_tables,
+                      block_table_stride,      cu_seqlens_q,   context_lens, num_seqs,
+                      max_query_len,           max_kv_len,     total_query_rows,
+                      scale,     causal,       num_heads,      k_scale,      v_scale};
+  const bool f8 = cache_dtype == VPA_DTYPE_FP8_E4M3;
   if (dtype == VPA_DTYPE_BF16)
-    return dispatch_dim<bf16_t>(group, out, query, key_cache, value_cache, block_tables,
-                                block_table_stride, cu_seqlens_q, context_lens, num_seqs,
-                                max_query_len, max_kv_len, total_query_rows, scale, causal,
-                                num_heads, g, stream);
+    return f8 ? dispatch_shape<bf16_t, fp8_t>(group, a, g, stream)
+              : dispatch_shape<bf16_t, bf16_t>(group, a, g, stream);
   if (dtype == VPA_DTYPE_F16)
-    return dispatch_dim<f16_t>(group, out, query, key_cache, value_cache, block_tables,
-                               block_table_stride, cu_seqlens_q, context_lens, num_seqs,
-                               max_query_len, max_kv_len, total_query_rows, scale, causal,
-                               num_heads, g, stream);
+    return f8 ? dispatch_shape<f16_t, fp8_t>(group, a, g, stream)
+              : dispatch_shape<f16_t, f16_t>(group, a, g, stream);
   return hipErrorInvalidValue;
 }
 

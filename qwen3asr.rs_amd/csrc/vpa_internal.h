@@ -82,18 +82,19 @@ hipError_t launch_paged_decode(int dtype, int cache_dtype, void* out, const void
                                int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
                                const DecodeWorkspace& ws, hipStream_t stream);
 
-hipError_t launch_prefill_paged(int dtype, void* out, const void* query, const void* key_cache,
-                                const void* value_cache, const uint32_t* block_tables,
-                                int32_t block_table_stride, const uint32_t* cu_seqlens_q,
-                                const uint32_t* context_lens, int32_t num_seqs,
-                                int32_t max_query_len, int32_t max_kv_len,
+hipError_t launch_prefill_paged(int dtype, int cache_dtype, void* out, const void* query,
+                                const void* key_cache, const void* value_cache,
+                                const uint32_t* block_tables, int32_t block_table_stride,
+                                const uint32_t* cu_seqlens_q, const uint32_t* context_lens,
+                                int32_t num_seqs, int32_t max_query_len, int32_t max_kv_len,
                                 int64_t total_query_rows, float scale, int32_t causal,
-                                int32_t num_heads, const CacheGeom& g, hipStream_t stream);
+                                int32_t num_heads, const CacheGeom& g, const float* k_scale,
+                                const float* v_scale, hipStream_t stream);
 
 // Query positions one prefill workgroup covers for a GQA group size.
 int prefill_positions_per_workgroup(int group);
 // True when the MFMA prefill kernel is compiled for this combination.
-bool prefill_supported(int dtype, int head_dim, int block_size, int group);
+bool prefill_supported(int dtype, int cache_dtype, int head_dim, int block_size, int group);
 
 // Builds the decode work list into the workspace (the plan launch of
 // launch_paged_decode on its own); a no-op for configurations whose decode

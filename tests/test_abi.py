@@ -310,5 +310,12 @@ def test_gather_and_prefill_fp8_validation():
     assert lib.vpa_gather_kv_cache(*args) == _lib.VPA_ERR_UNSUPPORTED  # 16-bit cache -> other
     args[17], args[18], args[9] = FP8, FP8, 0  # fp8 -> fp8 (raw bytes), empty batch
     assert lib.vpa_gather_kv_cache(*args) == 0, lib.vpa_last_error().decode()
-    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE)
-    assert rc == _lib.VPA_ERR_UNSUPPORTED and "differs" in msg
+    # prefill over an fp8 cache: validation only (no device here)
+    rc, msg = pf_call(cdtype=FP8, **F8_STRIDES)
+    assert rc == _lib.VPA_ERR_INVALID_ARGUMENT and "k_scale" in msg, msg
+    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, dtype=_lib.DTYPE_F32, **F8_STRIDES)
+    assert rc == _lib.VPA_ERR_UNSUPPORTED and "differs" in msg, msg
+    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bstride=8 * 64 * 16, hstride=64 * 16)
+    assert rc == _lib.VPA_ERR_UNSUPPORTED and "no MFMA kernel" in msg, msg
+    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bstride=8 * 128 * 8, hstride=128 * 8)
+    assert rc == _lib.VPA_ERR_UNSUPPORTED and "no MFMA kernel" in msg, msg

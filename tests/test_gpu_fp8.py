@@ -10,7 +10,10 @@
   kernel shares);
 * paged_attention over an fp8 cache: the fp64 oracle over the dequantised
   cache (the reference's fp8 semantics, prefill_paged_attn.metal:698-769),
-  bf16/f16 tolerance 2e-2, with stale NaN bytes past each context.
+  bf16/f16 tolerance 2e-2, with stale NaN bytes past each context;
+* chunked prefill over an fp8 cache: the fp64 oracle (causal and not,
+  scales, absent blocks, NaN bytes in every unused slot), and with scales 1
+  bit-equal to the bf16 kernel over a bf16 copy of the cache.
 """
 
 import numpy as np
@@ -197,3 +200,138 @@ def test_fp8_append_then_decode_end_to_end(device):
     want = orc.paged_attention(q, kc, vc, bt, np.array(lens), max(lens), d ** -0.5,
                                dtype=orc.BF16, kv_dtype=orc.FP8)
     assert_attention_close(orc.to_f32(to_host(out), orc.BF16), want, orc.BF16, "fp8 e2e")
+
+
+# ---- chunked prefill over an fp8 cache ----------------------------------------
+
+def fp8_prefill_case(device, code, h, kvh, bs, prior, qlens, seed, causal=True,
+                     scales=(1.0, 1.0), mutate_bt=None):
+    """Random fp8 caches with NaN bytes (0x7F) in every slot no sequence
+    holds; returns (kernel output as f32, fp64 oracle, inputs)."""
+    rng = np.random.default_rng(seed)
+    d = 128
+    ks, vs = scales
+    prior = np.asarray(prior, dtype=np.int64)
+    qlens = np.asarray(qlens, dtype=np.int64)
+    lens = prior + qlens
+    nb = int(sum((int(L) + bs - 1) // bs for L in lens)) + 6
+    kc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d // 16, bs, 16)) * 2).astype(np.float32))
+    vc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d, bs)) * 2).astype(np.float32))
+    bt = block_tables_for(rng, [max(int(L), 1) for L in lens], nb, bs)
+    used = np.zeros((nb, bs), dtype=bool)
+    for s, L in enumerate(lens):
+        t = np.arange(int(L))
+        used[bt[s, t // bs], t % bs] = True
+    kc[~used[:, None, None, :, None].repeat(kvh, 1).repeat(d // 16, 2).repeat(16, 4)] = 0x7F
+    vc[~used[:, None, None, :].repeat(kvh, 1).repeat(d, 2)] = 0x7F
+    if mutate_bt is not None:
+        mutate_bt(bt)
+    q = random_words(rng, (int(qlens.sum()), h, d), code)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.uint32)
+    lens32 = lens.astype(np.uint32)
+    scale = d ** -0.5
+    out = vpa.paged_attention_varlen_prefill(
+        to_dev(q, code, device), f8(kc, device), f8(vc, device), u32(bt, device),
+        u32(lens32, device), u32(cu, device), scalar(ks, device), scalar(vs, device), scale, 1.0,
+        causal=causal)
+    torch.cuda.synchronize()
+    want = orc.prefill_attention(q, kc, vc, bt, lens32, cu, scale, causal=causal, dtype=code,
+                                 kv_dtype=orc.FP8, k_scale=ks, v_scale=vs)
+    return orc.to_f32(to_host(out), code), want, (q, kc, vc, bt, lens32, cu, scale)
+
+
+PF_PRIOR = [0, 5, 31, 100, 0, 333]
+PF_NEW = [1, 31, 32, 33, 129, 70]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("bs", [16, 32])
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+def test_fp8_prefill_qwen3_asr_shape(device, code, bs, causal):
+    got, want, _ = fp8_prefill_case(device, code, 16, 8, bs, PF_PRIOR, PF_NEW,
+                                    seed=3 * bs + code + causal, causal=causal)
+    assert_attention_close(got, want, code, f"fp8 prefill code={code} bs={bs} causal={causal}")
+
+
+@pytest.mark.parametrize("h,kvh", [(8, 8), (16, 4)])
+def test_fp8_prefill_groups(device, h, kvh):
+    got, want, _ = fp8_prefill_case(device, orc.BF16, h, kvh, 16, [7, 0, 260], [40, 65, 17],
+                                    seed=h + kvh)
+    assert_attention_close(got, want, orc.BF16, f"fp8 prefill h={h} kvh={kvh}")
+
+
+@pytest.mark.parametrize("scales", [(0.37, 3.1), (4.0, 0.25), (-0.5, 1.5)])
+def test_fp8_prefill_scales(device, scales):
+    """k_scale folds into the softmax scale (a negative one flips which key
+    dominates), v_scale into the output."""
+    got, want, _ = fp8_prefill_case(device, orc.BF16, 16, 8, 16, [300, 0, 45], [90, 200, 1],
+                                    seed=int(10 * scales[0]) + 60, scales=scales)
+    assert_attention_close(got, want, orc.BF16, f"fp8 prefill scales={scales}")
+
+
+def test_fp8_prefill_absent_blocks(device):
+    def mutate(bt):
+        bt[0, 1] = 1 << 30     # out of the pool: its tokens are absent
+        bt[1, 0] = 0xFFFFFFFF
+    got, want, _ = fp8_prefill_case(device, orc.BF16, 16, 8, 16, [40, 20], [30, 50], seed=15,
+                                    mutate_bt=mutate)
+    assert_attention_close(got, want, orc.BF16, "fp8 prefill absent blocks")
+
+
+def test_fp8_prefill_equals_bf16_prefill_over_dequantised_cache(device):
+    """Scales 1: E4M3 values are exact in bf16, so the fp8 kernel feeds the
+    MFMAs the same operands as the bf16 kernel over a bf16 copy of the cache
+    (re-packed from 16 to 8 elements per key vector): the outputs are equal
+    bit for bit."""
+    code, h, kvh, bs = orc.BF16, 16, 8, 16
+    got, _, (q, kc, vc, bt, lens, cu, scale) = fp8_prefill_case(
+        device, code, h, kvh, bs, [0, 17, 500], [64, 33, 90], seed=21)
+    nb, _, c16, _, _ = kc.shape
+    d = c16 * 16
+    kf = orc.fp8_to_f32(kc).transpose(0, 1, 3, 2, 4).reshape(nb, kvh, bs, d)
+    kb = orc.from_f32(np.ascontiguousarray(
+        kf.reshape(nb, kvh, bs, d // 8, 8).transpose(0, 1, 3, 2, 4)), code)
+    vb = orc.from_f32(orc.fp8_to_f32(vc), code)
+    ref = vpa.paged_attention_varlen_prefill(
+        to_dev(q, code, device), to_dev(kb, code, device), to_dev(vb, code, device),
+        u32(bt, device), u32(lens, device), u32(cu, device), None, None, scale, 1.0,
+        causal=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.view(np.uint32), orc.to_f32(to_host(ref), code).view(np.uint32))
+
+
+def test_fp8_append_then_prefill_end_to_end(device):
+    """The new tokens appended into the fp8 cache, then prefill over it:
+    the cache bytes equal the oracle's encode and the attention its fp64
+    attention over the dequantised cache."""
+    rng = np.random.default_rng(31)
+    code, h, kvh, d, bs = orc.BF16, 16, 8, 128, 16
+    prior, new = np.array([20, 0, 130]), np.array([45, 70, 16])
+    lens = prior + new
+    nb = int(sum((int(L) + bs - 1) // bs for L in lens)) + 3
+    kc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d // 16, bs, 16))).astype(np.float32))
+    vc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d, bs))).astype(np.float32))
+    bt = block_tables_for(rng, lens, nb, bs)
+    slots = np.concatenate([bt[s, np.arange(P, L) // bs].astype(np.int64) * bs
+                            + np.arange(P, L) % bs for s, (P, L) in enumerate(zip(prior, lens))])
+    tq = int(new.sum())
+    k = random_words(rng, (tq, kvh, d), code)
+    v = random_words(rng, (tq, kvh, d), code)
+    q = random_words(rng, (tq, h, d), code)
+    ks, vs = 0.5, 0.75
+    kcd, vcd = f8(kc, device), f8(vc, device)
+    ksd, vsd = scalar(ks, device), scalar(vs, device)
+    vpa.reshape_and_cache(to_dev(k, code, device), to_dev(v, code, device), ksd, vsd, kcd, vcd,
+                          i64(slots, device))
+    cu = np.concatenate([[0], np.cumsum(new)]).astype(np.uint32)
+    out = vpa.paged_attention_varlen_prefill(
+        to_dev(q, code, device), kcd, vcd, u32(bt, device), u32(lens.astype(np.uint32), device),
+        u32(cu, device), ksd, vsd, d ** -0.5, 1.0, causal=True)
+    torch.cuda.synchronize()
+    orc.reshape_and_cache_fp8(k, v, kc, vc, slots, code, ks, vs)
+    np.testing.assert_array_equal(f8_host(kcd), kc)
+    np.testing.assert_array_equal(f8_host(vcd), vc)
+    want = orc.prefill_attention(q, kc, vc, bt, lens.astype(np.uint32), cu, d ** -0.5,
+                                 causal=True, dtype=code, kv_dtype=orc.FP8, k_scale=ks,
+                                 v_scale=vs)
+    assert_attention_close(orc.to_f32(to_host(out), code), want, code, "fp8 append + prefill")
