@@ -266,7 +266,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
 // chunks per key row).
 //
 // Work list: decode_plan_kernel (one workgroup) turns context_lens into the
-// sequence-ordered list of (sequence, chunk) items, a chunk being NW * PT
+// list of (sequence, chunk) items, longest first, a chunk being NW * PT
 // tokens, plus the list of sequences that span several chunks and a small
 // header {0, item count, multi count}. All of it lives in the caller's
 // workspace and is rebuilt by every call, so the launches can be captured
@@ -305,29 +305,24 @@ __device__ __forceinline__ int clamp_context(uint32_t ctx, int max_ctx, int cap)
   return min((int)min(ctx, (uint32_t)max_ctx), cap);
 }
 
-// Item order. With 16-bit caches items stay in sequence order: long and
-// short chunks interleave over the whole launch, and the short ones, whose
-// waves are latency-bound, overlap the streaming of the long ones (grouping
-// them measured slower). With fp8 caches (two long waves per workgroup)
-// items are emitted longest first, a counting sort over kPlanMaxBuckets
-// classes of chunk length, stable within a class: measured 9 % faster.
-constexpr int kPlanMaxBuckets = 8;
+// Items are emitted longest first: a counting sort over kPlanBuckets
+// classes of chunk length, stable within a class, so full chunks start
+// first and the last workgroups the dispatcher hands out are short, which
+// keeps the launch's tail short (measured on c3: 8 classes beat 2, 4 and
+// 16, and sequence order).
+constexpr int kPlanBuckets = 8;
 
-__host__ __device__ constexpr int plan_buckets(bool fp8_cache) {
-  return fp8_cache ? kPlanMaxBuckets : 1;
-}
-
-__device__ __forceinline__ int plan_bucket(int L, int p, int part_tokens, int buckets) {
-  if (L <= 0) return buckets - 1;
+__device__ __forceinline__ int plan_bucket(int L, int p, int part_tokens) {
+  if (L <= 0) return kPlanBuckets - 1;
   const int n = min(part_tokens, L - p * part_tokens);  // tokens of chunk p, >= 1
-  return (int)(((int64_t)(part_tokens - n) * buckets) / part_tokens);
+  return (int)(((int64_t)(part_tokens - n) * kPlanBuckets) / part_tokens);
 }
 
 __global__ __launch_bounds__(1024) void decode_plan_kernel(
     const uint32_t* __restrict__ context_lens, int32_t num_seqs, int32_t max_ctx,
-    int32_t cap_tokens, int32_t part_tokens, int32_t buckets, uint2* __restrict__ items,
+    int32_t cap_tokens, int32_t part_tokens, uint2* __restrict__ items,
     uint32_t* __restrict__ multi, uint32_t* __restrict__ queue) {
-  constexpr int NB = kPlanMaxBuckets;
+  constexpr int NB = kPlanBuckets;
   __shared__ uint32_t s_wave[16][NB];
   __shared__ uint32_t s_base[NB + 1];
   __shared__ uint32_t s_multi;
@@ -344,7 +339,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(
     const int L = clamp_context(context_lens[s], max_ctx, cap_tokens);
     const int n = L > 0 ? (L + part_tokens - 1) / part_tokens : 1;
     for (int p = 0; p < n; ++p) {
-      const int b = plan_bucket(L, p, part_tokens, buckets);
+      const int b = plan_bucket(L, p, part_tokens);
 #pragma unroll
       for (int c = 0; c < NB; ++c) cnt[c] += c == b;
     }
@@ -383,7 +378,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(
     const int L = clamp_context(context_lens[s], max_ctx, cap_tokens);
     const int n = L > 0 ? (L + part_tokens - 1) / part_tokens : 1;
     for (int p = 0; p < n; ++p) {
-      const int b = plan_bucket(L, p, part_tokens, buckets);
+      const int b = plan_bucket(L, p, part_tokens);
       uint32_t at = 0;
 #pragma unroll
       for (int c = 0; c < NB; ++c)
@@ -813,22 +808,34 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
   }
 }
 
+// 16-bit caches: 4 waves of up to 512 tokens per 2048-token chunk (measured
+// on c3 with the longest-first plan: 172.5 us per layer; 8 x 512 174.2,
+// 4 x 448 173.0, 4 x 384 174.0, 4 x 256 174.7, 6 x 512 179.7; 8 x 128 in
+// sequence order 175.5)
 #ifndef VPA_DECODE_ROWS_PT
-#define VPA_DECODE_ROWS_PT 128
+#define VPA_DECODE_ROWS_PT 512
 #endif
 #ifndef VPA_DECODE_ROWS_WAVES
-#define VPA_DECODE_ROWS_WAVES 8
+#define VPA_DECODE_ROWS_WAVES 4
 #endif
 constexpr int kRowsPT = VPA_DECODE_ROWS_PT;  // partition tokens per wave of the rows kernel
 constexpr int kRowsWaves = VPA_DECODE_ROWS_WAVES;  // waves (partitions) per workgroup
-// fp8 caches: the same chunk (the plan is shared) over fewer, longer waves,
-// so that each wave keeps as many bytes in flight as a 16-bit one
+// fp8 caches: fewer, longer waves, so that each wave keeps as many bytes in
+// flight as a 16-bit one
 #ifndef VPA_DECODE_FP8_WAVES
 #define VPA_DECODE_FP8_WAVES 2
 #endif
+#ifndef VPA_DECODE_FP8_PT
+#define VPA_DECODE_FP8_PT 512
+#endif
 constexpr int kF8Waves = VPA_DECODE_FP8_WAVES;
-constexpr int kF8PT = kRowsPT * kRowsWaves / kF8Waves;
-static_assert(kRowsPT >= kDecodeMinPartitionTokens, "workspace sized for 128-token partitions");
+constexpr int kF8PT = VPA_DECODE_FP8_PT;
+static_assert(kRowsPT >= kDecodeMinPartitionTokens && kF8PT >= kDecodeMinPartitionTokens,
+              "workspace sized for 128-token partitions");
+// Tokens per work item (workgroup) of the plan, by cache type.
+__host__ __device__ constexpr int decode_chunk_tokens(bool fp8_cache) {
+  return fp8_cache ? kF8PT * kF8Waves : kRowsPT * kRowsWaves;
+}
 
 // Merge of split-K partials: persistent waves over (sequence, query head)
 // units; sequences of one chunk were written directly and are skipped. One
@@ -902,14 +909,13 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
   constexpr bool kFp8 = std::is_same_v<C, fp8_t>;
   constexpr int PT = kFp8 ? kF8PT : kRowsPT;
   constexpr int NW = kFp8 ? kF8Waves : kRowsWaves;
-  constexpr int kChunk = PT * NW;  // tokens per workgroup (the same for every cache type)
-  static_assert(kChunk == kRowsPT * kRowsWaves, "one plan serves every cache type");
+  constexpr int kChunk = PT * NW;  // tokens per workgroup
+  static_assert(kChunk == decode_chunk_tokens(kFp8), "the plan's chunk");
   const int cap_tokens = bts * g.block_size;
   hipError_t e = hipSuccess;
   if (!ws.planned) {
     hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, cl, num_seqs,
-                       max_ctx, cap_tokens, kChunk, plan_buckets(kFp8), ws.items, ws.multi,
-                       ws.queue);
+                       max_ctx, cap_tokens, kChunk, ws.items, ws.multi, ws.queue);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1046,9 +1052,9 @@ hipError_t launch_decode_plan(int dtype, int cache_dtype, const uint32_t* contex
   const bool rows = (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) && g.head_dim <= 128;
   if (!rows || num_seqs == 0) return hipSuccess;
   hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, context_lens, num_seqs,
-                     max_context_len, block_table_stride * g.block_size, kRowsPT * kRowsWaves,
-                     plan_buckets(cache_dtype == VPA_DTYPE_FP8_E4M3), ws.items, ws.multi,
-                     ws.queue);
+                     max_context_len, block_table_stride * g.block_size,
+                     decode_chunk_tokens(cache_dtype == VPA_DTYPE_FP8_E4M3), ws.items,
+                     ws.multi, ws.queue);
   return hipGetLastError();
 }
 
