@@ -18,10 +18,12 @@ from .ops import (  # noqa: F401
     paged_attention_workspace,
     reshape_and_cache,
 )
+from .step import DeviceDecodeStep  # noqa: F401
 
 __all__ = [
     "DecodeTokenState",
     "DeviceBlockAllocator",
+    "DeviceDecodeStep",
     "VpaError",
     "argmax_token_ids_from_logits",
     "cache_geometry",
