@@ -59,6 +59,8 @@ def parse():
                     help="skip the c4 chunked-prefill measurement")
     ap.add_argument("--no-fp8", dest="fp8", action="store_false",
                     help="skip the fp8-cache decode measurement")
+    ap.add_argument("--no-device-step", dest="device_step", action="store_false",
+                    help="skip the device-resident whole-step measurement")
     return ap.parse_args()
 
 
@@ -288,6 +290,129 @@ def decode_fp8(w, dev, reps):
             "gbps": round(gbps, 2), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
+def device_step(w, dev, reps, warmup):
+    """The whole decode step kept on the device (vpa.DeviceDecodeStep) on c3's
+    batch and lengths: token bookkeeping, block growth and step metadata,
+    the work list, 28 x (append + attention) and the argmax over a
+    [256, 151936] logits buffer, captured as one HIP graph and replayed back
+    to back. Beside it the same step driven from the host the way the
+    reference's loop runs it (paged_batch_engine.rs:629-722): read the ids
+    back, EOS bookkeeping on the host, grow blocks with the host block
+    manager, upload slot_mapping / context_lens / block tables, then replay
+    a graph of the device work (work list, layers, argmax). The layers
+    share one block table (one block manager per model), each with its own
+    cache pool. Host work here is this package's host mirror (numpy and
+    the C++ block manager through ctypes), slower than the reference's Rust
+    loop; the device step's figure does not depend on it."""
+    import numpy as np
+    import torch
+
+    import vpa
+    from vpa import host
+
+    B, H, KVH, D, BS = w.num_seqs, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    vocab, eos = 151936, [151643, 151645]  # Qwen3 vocabulary, <|endoftext|> / <|im_end|>
+    n_steps = 2 * (reps + warmup) + 4
+    prompts = (w.context_lens.astype(np.int64) - 1)
+    max_ctx = int(prompts.max()) + n_steps + 1
+    need = int(((prompts + n_steps + BS) // BS).sum())
+    nb = need + 1 + need // 8
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev)
+    g.manual_seed(w.seed + 2)
+    layers = [dict(kc=torch.randn((nb, KVH, D // 8, BS, 8), generator=g, device=dev, dtype=bf),
+                   vc=torch.randn((nb, KVH, D, BS), generator=g, device=dev, dtype=bf),
+                   q=torch.randn((B, H, D), generator=g, device=dev, dtype=bf),
+                   k=torch.randn((B, KVH, D), generator=g, device=dev, dtype=bf),
+                   v=torch.randn((B, KVH, D), generator=g, device=dev, dtype=bf),
+                   out=torch.empty((B, H, D), device=dev, dtype=bf)) for _ in range(len(w.layers))]
+    logits = torch.randn((B, vocab), generator=g, device=dev, dtype=bf)
+    st = vpa.DeviceDecodeStep(B, nb, BS, max_ctx, H, D, eos, n_steps + 1, dev)
+    st.admit(torch.from_numpy(prompts.astype(np.uint32)).to(dev))
+    L0 = layers[0]
+
+    def work():  # the device work of a step after its metadata
+        vpa.paged_attention_plan(st.allocator.context_lens, max_ctx, st.cols, H, L0["kc"],
+                                 L0["vc"], bf, st.workspace)
+        for L in layers:
+            st.layer(L["q"], L["k"], L["v"], L["kc"], L["vc"], L["out"])
+        st.end(logits)
+
+    def full():
+        st.tokens.consume()
+        st.allocator.step(st.tokens.finished)
+        work()
+
+    torch.cuda.synchronize()
+    g_full, g_work = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_full):
+        full()
+    with torch.cuda.graph(g_work):
+        work()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        g_full.replay()
+    dev_ms = timed_ms(g_full.replay, reps)
+
+    # host-driven: the host block manager follows the device allocator's state
+    mgr = host.BlockManager(nb, BS)
+    pos = (st.allocator.positions.cpu().numpy().astype(np.int64))
+    tables = st.allocator.block_tables.cpu().numpy()
+    nblk = st.allocator.row_blocks.cpu().numpy().astype(np.int64)
+    fin = st.tokens.finished.cpu().numpy().astype(bool)
+    for r in range(B):
+        assert mgr.try_allocate_slots(r, int(nblk[r]) * BS)
+        tables[r, :nblk[r]] = mgr.block_ids(r)  # same FIFO order as the ring: ids differ
+    st.allocator.block_tables.copy_(torch.from_numpy(tables))
+    pin = dict(slots=torch.empty(B, dtype=torch.int64).pin_memory(),
+               ctx=torch.empty(B, dtype=torch.uint32).pin_memory(),
+               tables=torch.empty(tables.shape, dtype=torch.uint32).pin_memory(),
+               ids=torch.empty(B, dtype=torch.uint32).pin_memory())
+    eos_arr = np.array(eos, dtype=np.uint32)
+    generated = [[] for _ in range(B)]
+
+    def host_step():
+        ids = pin["ids"]
+        ids.copy_(st.tokens.next_ids)  # read-back: waits for the previous step
+        idv = ids.numpy()
+        hit = np.isin(idv, eos_arr) & ~fin
+        fin[hit] = True
+        for r in np.flatnonzero(~fin):
+            generated[r].append(int(idv[r]))
+        slots = np.full(B, -1, dtype=np.int64)
+        ctx = np.ones(B, dtype=np.uint32)
+        for r in np.flatnonzero(~fin):
+            p = int(pos[r])
+            if p // BS >= nblk[r]:
+                if not mgr.try_allocate_slots(r, p + 1):
+                    continue
+                tables[r, nblk[r]] = mgr.block_ids(r)[-1]
+                nblk[r] += 1
+            slots[r] = int(tables[r, p // BS]) * BS + p % BS
+            ctx[r] = p + 1
+            pos[r] = p + 1
+        pin["slots"].numpy()[:] = slots
+        pin["ctx"].numpy()[:] = ctx
+        pin["tables"].numpy()[:] = tables
+        st.allocator.slot_mapping.copy_(pin["slots"], non_blocking=True)
+        st.allocator.context_lens.copy_(pin["ctx"], non_blocking=True)
+        st.allocator.block_tables.copy_(pin["tables"], non_blocking=True)
+        g_work.replay()
+
+    for _ in range(warmup):
+        host_step()
+    host_ms = timed_ms(host_step, reps)
+    del layers, logits, st, g_full, g_work
+    torch.cuda.empty_cache()
+    return {"workload": w.name, "layers": len(w.layers), "vocab": vocab,
+            "device_resident_ms_per_step": round(dev_ms, 4),
+            "host_driven_ms_per_step": round(host_ms, 4),
+            "what": "one decode step: bookkeeping + block growth + metadata + work list + "
+                    "28 x (append + attention) + argmax; device-resident = one graph replay "
+                    "per step, no host read; host-driven = ids read back, host bookkeeping and "
+                    "block manager, metadata upload, then a graph of the device work"}
+
+
 def prefill_c4(dev, reps=10):
     """Row a3 measured alongside the headline: c4 (64 sequences x 512 new
     tokens over 0..1024 prior tokens, bf16) append with reshape_and_cache,
@@ -445,6 +570,9 @@ def main():
     f8 = None
     if args.fp8 and w.dtype == "bf16":
         f8 = decode_fp8(w, dev, args.steps)
+    dstep = None
+    if args.device_step and w.name == "c3":
+        dstep = device_step(w, dev, args.steps, args.warmup)
     pf = None
     if args.prefill:
         pf = prefill_c4(dev)
@@ -496,6 +624,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "decode_fp8": f8,
+        "device_step": dstep,
         "prefill_c4": pf,
     }
     print(json.dumps(line), flush=True)
