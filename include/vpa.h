@@ -160,17 +160,17 @@ int vpa_paged_attention(void* out, const void* query, const float* k_scale,
  * step (vASR calls paged_attention once per decoder layer with the same
  * block tables and context lengths, thinker_text.rs:1126-1139, so the list
  * is per-step metadata like them). Arguments mean what they mean in
- * vpa_paged_attention (cache_dtype: the caches' type, which orders the
- * list); the workspace is that call's. Stream-ordered and capture-safe; a
- * no-op for configurations whose kernel needs no list.
+ * vpa_paged_attention (dtype: the query type; the list is the same for
+ * every cache type); the workspace is that call's. Stream-ordered and
+ * capture-safe; a no-op for configurations whose kernel needs no list.
  * No counterpart in the reference (its decode kernel sizes its grid from
  * max_context_len only).
  */
 int vpa_paged_attention_plan(const uint32_t* context_lens, int32_t max_context_len,
                              int32_t block_table_stride, int32_t num_seqs, int32_t num_heads,
                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                             int32_t dtype, int32_t cache_dtype, void* workspace,
-                             size_t workspace_bytes, void* stream);
+                             int32_t dtype, void* workspace, size_t workspace_bytes,
+                             void* stream);
 
 /*
  * paged_attention_planned — vpa_paged_attention without the work-list

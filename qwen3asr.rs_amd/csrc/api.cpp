@@ -375,14 +375,10 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
 int vpa_paged_attention_plan(const uint32_t* context_lens, int32_t max_context_len,
                              int32_t block_table_stride, int32_t num_seqs, int32_t num_heads,
                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                             int32_t dtype, int32_t cache_dtype, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+                             int32_t dtype, void* workspace, size_t workspace_bytes,
+                             void* stream) {
   clear_error();
   const char* op = "paged_attention_plan";
-  if (dtype != cache_dtype && !(cache_dtype == VPA_DTYPE_FP8_E4M3 &&
-                                (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16)))
-    return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from query dtype %s", op,
-                dtype_name(cache_dtype), dtype_name(dtype));
   if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
       max_context_len < 0 || block_table_stride < 0 || num_heads % num_kv_heads != 0)
     return fail(VPA_ERR_INVALID_ARGUMENT,
@@ -413,7 +409,7 @@ int vpa_paged_attention_plan(const uint32_t* context_lens, int32_t max_context_l
   CacheGeom g{num_kv_heads, head_dim, block_size, 1, 0, 0};
   DecodeWorkspace ws =
       carve_decode_workspace(workspace, num_seqs, num_heads, head_dim, max_context_len);
-  return hip_status(op, launch_decode_plan(dtype, cache_dtype, context_lens, max_context_len,
+  return hip_status(op, launch_decode_plan(dtype, context_lens, max_context_len,
                                            block_table_stride, num_seqs, g, ws,
                                            static_cast<hipStream_t>(stream)));
 }

@@ -820,10 +820,11 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
 #endif
 constexpr int kRowsPT = VPA_DECODE_ROWS_PT;  // partition tokens per wave of the rows kernel
 constexpr int kRowsWaves = VPA_DECODE_ROWS_WAVES;  // waves (partitions) per workgroup
-// fp8 caches: fewer, longer waves, so that each wave keeps as many bytes in
-// flight as a 16-bit one
+// fp8 caches: the same chunk, so one work list serves every cache type
+// (measured on c3, us per layer: 4 x 512 101.7, 2 x 1024 103.6, 2 x 768 105.8,
+// 1 x 1024 107.1; 2 x 512 over 1024-token chunks 102.6)
 #ifndef VPA_DECODE_FP8_WAVES
-#define VPA_DECODE_FP8_WAVES 2
+#define VPA_DECODE_FP8_WAVES 4
 #endif
 #ifndef VPA_DECODE_FP8_PT
 #define VPA_DECODE_FP8_PT 512
@@ -832,10 +833,9 @@ constexpr int kF8Waves = VPA_DECODE_FP8_WAVES;
 constexpr int kF8PT = VPA_DECODE_FP8_PT;
 static_assert(kRowsPT >= kDecodeMinPartitionTokens && kF8PT >= kDecodeMinPartitionTokens,
               "workspace sized for 128-token partitions");
-// Tokens per work item (workgroup) of the plan, by cache type.
-__host__ __device__ constexpr int decode_chunk_tokens(bool fp8_cache) {
-  return fp8_cache ? kF8PT * kF8Waves : kRowsPT * kRowsWaves;
-}
+// Tokens per work item (workgroup) of the plan.
+constexpr int kDecodeChunk = kRowsPT * kRowsWaves;
+static_assert(kF8PT * kF8Waves == kDecodeChunk, "one work list serves every cache type");
 
 // Merge of split-K partials: persistent waves over (sequence, query head)
 // units; sequences of one chunk were written directly and are skipped. One
@@ -910,7 +910,7 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
   constexpr int PT = kFp8 ? kF8PT : kRowsPT;
   constexpr int NW = kFp8 ? kF8Waves : kRowsWaves;
   constexpr int kChunk = PT * NW;  // tokens per workgroup
-  static_assert(kChunk == decode_chunk_tokens(kFp8), "the plan's chunk");
+  static_assert(kChunk == kDecodeChunk, "the plan's chunk");
   const int cap_tokens = bts * g.block_size;
   hipError_t e = hipSuccess;
   if (!ws.planned) {
@@ -1045,15 +1045,13 @@ hipError_t dispatch_decode(int dtype, int D, int BS, int group, A... args) {
 
 }  // namespace
 
-hipError_t launch_decode_plan(int dtype, int cache_dtype, const uint32_t* context_lens,
-                              int32_t max_context_len, int32_t block_table_stride,
-                              int32_t num_seqs, const CacheGeom& g, const DecodeWorkspace& ws,
-                              hipStream_t stream) {
+hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t max_context_len,
+                              int32_t block_table_stride, int32_t num_seqs, const CacheGeom& g,
+                              const DecodeWorkspace& ws, hipStream_t stream) {
   const bool rows = (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) && g.head_dim <= 128;
   if (!rows || num_seqs == 0) return hipSuccess;
   hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, context_lens, num_seqs,
-                     max_context_len, block_table_stride * g.block_size,
-                     decode_chunk_tokens(cache_dtype == VPA_DTYPE_FP8_E4M3), ws.items,
+                     max_context_len, block_table_stride * g.block_size, kDecodeChunk, ws.items,
                      ws.multi, ws.queue);
   return hipGetLastError();
 }

@@ -99,10 +99,9 @@ bool prefill_supported(int dtype, int cache_dtype, int head_dim, int block_size,
 // Builds the decode work list into the workspace (the plan launch of
 // launch_paged_decode on its own); a no-op for configurations whose decode
 // kernel takes no work list.
-hipError_t launch_decode_plan(int dtype, int cache_dtype, const uint32_t* context_lens,
-                              int32_t max_context_len, int32_t block_table_stride,
-                              int32_t num_seqs, const CacheGeom& g, const DecodeWorkspace& ws,
-                              hipStream_t stream);
+hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t max_context_len,
+                              int32_t block_table_stride, int32_t num_seqs, const CacheGeom& g,
+                              const DecodeWorkspace& ws, hipStream_t stream);
 
 // Next-token ids of `num_rows` logits rows (first maximum, NaN-aware as
 // candle's argmax) and the step-start EOS bookkeeping of the decode loop.

@@ -48,7 +48,7 @@ SIGNATURES = {
                                            _f32, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i64,
                                            _i64, _i32, _i32, _p, _sz, _p]),
     "vpa_paged_attention_plan": (ctypes.c_int, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-                                                _i32, _i32, _p, _sz, _p]),
+                                                _i32, _p, _sz, _p]),
     "vpa_paged_attention_planned": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32,
                                                    _f32, _f32, _p, _i32, _i32, _i32, _i32, _i32,
                                                    _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),

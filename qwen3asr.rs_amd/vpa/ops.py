@@ -208,8 +208,7 @@ def paged_attention_plan(context_lens: torch.Tensor, max_context_len: int,
         raise _err(f"context_lens must be u32 1-d, got {context_lens.dtype}")
     check(_lib.load().vpa_paged_attention_plan(
         context_lens.contiguous().data_ptr(), int(max_context_len), int(block_table_stride),
-        context_lens.shape[0], num_heads, kvh, d, bs, dtype_code(dtype),
-        dtype_code(key_cache.dtype), workspace.data_ptr(),
+        context_lens.shape[0], num_heads, kvh, d, bs, dtype_code(dtype), workspace.data_ptr(),
         workspace.numel() * workspace.element_size(), _stream(context_lens)))
 
 

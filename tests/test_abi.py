@@ -205,8 +205,7 @@ def test_prefill_empty_is_noop():
 
 def plan_call(**over):
     args = dict(cl=FAKE, max_ctx=1024, bts=64, b=4, h=16, kvh=8, d=128, bs=16,
-                dtype=_lib.DTYPE_BF16, cdtype=_lib.DTYPE_BF16, ws=FAKE * 256, ws_bytes=1 << 30,
-                stream=None)
+                dtype=_lib.DTYPE_BF16, ws=FAKE * 256, ws_bytes=1 << 30, stream=None)
     args.update(over)
     lib = _lib.load()
     rc = lib.vpa_paged_attention_plan(*args.values())
@@ -222,9 +221,6 @@ def plan_call(**over):
     (dict(cl=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
     (dict(bts=10), _lib.VPA_ERR_INVALID_ARGUMENT, "block_table_stride"),
     (dict(b=70000), _lib.VPA_ERR_UNSUPPORTED, "num_seqs"),
-    (dict(cdtype=_lib.DTYPE_F16), _lib.VPA_ERR_UNSUPPORTED, "cache dtype"),
-    (dict(dtype=_lib.DTYPE_F32, cdtype=_lib.DTYPE_FP8_E4M3), _lib.VPA_ERR_UNSUPPORTED,
-     "cache dtype"),
 ])
 def test_paged_attention_plan_host_validation(over, code, needle):
     rc, msg = plan_call(**over)
