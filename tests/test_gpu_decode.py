@@ -148,6 +148,26 @@ def test_decode_config_c3_layer(device):
     assert_attention_close(got, want, code, f"c3 sample {sample}")
 
 
+# lengths at the rows kernel's per-wave (512-token) and per-chunk
+# (2048-token) boundaries: partitions split over the waves, merges of 2..4
+# chunks, a chunk whose last wave holds one token
+CHUNK_EDGES = [1, 511, 512, 513, 1535, 1536, 1537, 2047, 2048, 2049, 2050, 4095, 4096, 4097,
+               6144, 6145, 8191]
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_decode_chunk_and_wave_boundaries(device, code, bs):
+    got, want = decode_case(device, code, 16, 8, 128, bs, CHUNK_EDGES, seed=90 + bs + code)
+    assert_attention_close(got, want, code, f"edges code={code} bs={bs}")
+
+
+@pytest.mark.parametrize("h,kvh", [(8, 8), (16, 4)])
+def test_decode_chunk_boundaries_other_groups(device, h, kvh):
+    got, want = decode_case(device, orc.BF16, h, kvh, 128, 16, CHUNK_EDGES, seed=95 + h + kvh)
+    assert_attention_close(got, want, orc.BF16, f"edges h={h} kvh={kvh}")
+
+
 def test_decode_long_context_split_k(device):
     """Contexts spanning many split-K partitions (up to 8192 tokens)."""
     lens = [8192, 4097, 4096, 2049, 333]

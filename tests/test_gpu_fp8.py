@@ -156,6 +156,15 @@ def test_fp8_decode_qwen3_asr_shape(device, code, bs):
     assert_attention_close(got, want, code, f"fp8 code={code} bs={bs}")
 
 
+@pytest.mark.parametrize("bs", [16, 32])
+def test_fp8_decode_chunk_and_wave_boundaries(device, bs):
+    """Lengths at the per-wave (512-token) and per-chunk (2048-token)
+    boundaries of the rows kernel, merges of up to 4 chunks."""
+    lens = [1, 511, 512, 513, 2047, 2048, 2049, 4095, 4096, 4097, 6145, 8191]
+    got, want = fp8_decode_case(device, orc.BF16, 16, 8, 128, bs, lens, seed=200 + bs)
+    assert_attention_close(got, want, orc.BF16, f"fp8 edges bs={bs}")
+
+
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("h,kvh", [(8, 8), (16, 8), (16, 4)])
 def test_fp8_decode_head_dims_and_groups(device, d, h, kvh):
