@@ -18,9 +18,11 @@ from .ops import (  # noqa: F401
     paged_attention_workspace,
     reshape_and_cache,
 )
+from .graph import DecodeGraphCache  # noqa: F401
 from .step import DeviceDecodeStep  # noqa: F401
 
 __all__ = [
+    "DecodeGraphCache",
     "DecodeTokenState",
     "DeviceBlockAllocator",
     "DeviceDecodeStep",

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 from vpa import host
+from vpa.graph import DecodeGraphCache
 from vpa._lib import VPA_ERR_CAPACITY, VPA_ERR_INVALID_ARGUMENT, VPA_ERR_NOT_FOUND, VpaError
 
 PAD = host.PAD_SLOT_ID
@@ -303,3 +304,20 @@ def test_pad_decode_batch_kat():
     assert e.value.code == VPA_ERR_INVALID_ARGUMENT
     with pytest.raises(VpaError, match="down to"):
         host.pad_decode_batch_to_max(8, [1, 2, 3], [0, 0, 0], [1, 1, 1], bt, 2)
+
+
+def test_graph_cache_keys_follow_the_reference_buckets():
+    """Batch buckets 1, 2, 4, 8, then multiples of 16; columns a power of two
+    of at least 256 / block_size (cuda_graph.rs:28-81)."""
+    cache = DecodeGraphCache(lambda bufs, m: bufs["input_ids"], 256, 16, {}, "cpu")
+    assert cache.key(1, 1) == (1, 16)
+    assert cache.key(3, 16) == (4, 16)
+    assert cache.key(9, 17) == (16, 32)
+    assert cache.key(17, 100) == (32, 128)
+    assert cache.key(256, 300) == (256, 512)
+    assert host.cuda_graph_batch_buckets(40) == [1, 2, 4, 8, 16, 32, 40]
+    assert DecodeGraphCache(lambda b, m: b, 40, 16, {}, "cpu").key(33, 1) == (40, 16)
+    with pytest.raises(ValueError):
+        cache.key(257, 1)
+    with pytest.raises(ValueError):
+        cache.key(0, 1)
