@@ -91,7 +91,11 @@ __device__ __forceinline__ float max_xor32(float v) {
 #endif
 constexpr int kPrefillKeys = 32;                    // keys per tile
 constexpr int kPrefillStages = VPA_PREFILL_STAGES;  // LDS tile buffers (tiles in flight + 1)
-constexpr int kPrefillThreads = 256;
+#ifndef VPA_PREFILL_WAVES
+#define VPA_PREFILL_WAVES 4
+#endif
+constexpr int kPrefillWaves = VPA_PREFILL_WAVES;  // waves per workgroup, 32 query rows each
+constexpr int kPrefillThreads = 64 * kPrefillWaves;
 static_assert(kPrefillStages >= 2 && kPrefillStages <= 4, "stages");
 
 // s_waitcnt vmcnt(N), leaving the other counters alone (gfx9 encoding).
@@ -210,12 +214,14 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   constexpr int NS = kPrefillStages;
   constexpr int X = kF8 ? 16 : 8;  // cache elements per 16-byte unit
   constexpr int PPW = 32 / G;   // query positions per wave
-  constexpr int PPB = 4 * PPW;  // query positions per workgroup
+  constexpr int PPB = kPrefillWaves * PPW;  // query positions per workgroup
   constexpr int KS = D / 16;    // k-steps of Q.K^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
   constexpr int UB = BS / X;    // 16-byte units per value row of a block
   constexpr int NU = D * KT / X;                   // 16-byte units per K (and per V) tile
-  constexpr int DPW = NU / kPrefillThreads;        // DMAs per wave per K (and per V) tile
+  // DMAs per issuing wave per K (and per V) tile; the first DMW waves issue
+  constexpr int DPW = NU >= kPrefillThreads ? NU / kPrefillThreads : 1;
+  constexpr int DMW = NU / 64 / DPW;
   constexpr int DPT = 2 * DPW;                     // DMAs per wave per tile
   constexpr int NBT = KT / BS;                     // blocks per tile
   constexpr int RBV = D * UB;                      // units of one block's K (or V) rows
@@ -224,8 +230,8 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   // lanes of one LDS read pass span two blocks, padded to other banks
   constexpr int RBK = RBV + (BS == 8 ? 8 : 0);
   constexpr int KU = NBT * RBK;                    // K units of a stage
-  static_assert(KT % BS == 0 && BS >= 8 && NU % kPrefillThreads == 0 && RBV % 64 == 0 &&
-                    (kPrefillThreads / 64 * DPW) % DPB == 0,
+  static_assert(KT % BS == 0 && BS >= 8 && NU % 64 == 0 && DMW * DPW * 64 == NU &&
+                    DMW <= kPrefillWaves && RBV % 64 == 0 && (DMW * DPW) % DPB == 0,
                 "tile shape");
 
   // one LDS object per stage: the compiler then knows that a DMA into one
@@ -342,6 +348,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   // blocks read block 0 (in bounds); they are masked in S and their values
   // zeroed when the V operands are built.
   auto issue = [&](auto sc, int t) {
+    if (DMW < kPrefillWaves && wave >= DMW) return;  // wave issues no DMA (uniform)
     const int k0 = t * KT;
     uint32_t pb[NBT];
     tile_blocks(k0, pb);
@@ -595,7 +602,7 @@ struct PrefillArgs {
 
 template <typename T, typename C, int D, int BS, int G>
 hipError_t launch_prefill_t(const PrefillArgs& a, const CacheGeom& g, hipStream_t stream) {
-  constexpr int kPositions = 4 * 32 / G;
+  constexpr int kPositions = kPrefillWaves * 32 / G;
   const int q_tiles = (a.max_query_len + kPositions - 1) / kPositions;
   const int64_t grid = (int64_t)a.num_seqs * q_tiles * g.num_kv_heads;
   if (grid == 0) return hipSuccess;
@@ -659,7 +666,7 @@ bool prefill_supported(int dtype, int cache_dtype, int head_dim, int block_size,
          (block_size == 8 || block_size == 16 || block_size == 32);
 }
 
-int prefill_positions_per_workgroup(int group) { return 4 * 32 / group; }
+int prefill_positions_per_workgroup(int group) { return kPrefillWaves * 32 / group; }
 
 hipError_t launch_prefill_paged(int dtype, int cache_dtype, void* out, const void* query,
                                 const void* key_cache, const void* value_cache,
