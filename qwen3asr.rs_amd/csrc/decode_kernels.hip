@@ -426,12 +426,12 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(
 // *k_scale is folded into the softmax scale and *v_scale into the output.
 // Waves per SIMD the rows kernel is compiled for: instances with many q
 // vectors per lane (16-byte vectors: G x chunks per lane, two per chunk for
-// fp8) would spill at 3 (measured: fp8 at 16, 16-bit at 32).
+// fp8) would spill at 3 (with 512-token waves: 16 and more).
 template <typename C, int D, int BS, int G>
 constexpr int rows_waves_per_eu() {
   constexpr bool f8 = sizeof(C) == 1;
   constexpr int qvec = G * (D * BS / ((f8 ? 16 : 8) * 64)) * (f8 ? 2 : 1);
-  return (f8 ? qvec >= 16 : qvec > 16) ? 2 : VPA_DECODE_ROWS_WAVES_PER_EU;
+  return qvec >= 16 ? 2 : VPA_DECODE_ROWS_WAVES_PER_EU;
 }
 
 template <typename T, typename C, int D, int BS, int G, int PT, int NW>
