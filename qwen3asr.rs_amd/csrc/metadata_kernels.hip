@@ -189,15 +189,66 @@ __global__ __launch_bounds__(kMetaThreads) void release_blocks_kernel(
 // Grow rows, in index order, to hold target_tokens[r] tokens: each row takes
 // the blocks it lacks from the ring's head if all of them are there, else it
 // takes none and ok[r] = 0 (try_allocate_slots, paged_cache_runtime.rs:
-// 260-300, called row by row). One thread: the outcome of a row depends on
-// every row before it; admissions are rare next to steps.
-__global__ __launch_bounds__(64) void allocate_rows_kernel(
+// 260-300, called row by row); a row whose table is too narrow fails too.
+// When all rows' missing blocks fit (admission of a batch into a pool with
+// room), every row succeeds and row r takes the ring entries after those of
+// the rows before it: a workgroup prefix sum, then each row copies its ids.
+// Otherwise the outcome of a row depends on every row before it, and one
+// thread walks the rows.
+__device__ __forceinline__ uint32_t blocks_missing(const uint32_t* target_tokens,
+                                                   const uint32_t* row_blocks, int r,
+                                                   int32_t block_size, int32_t cols) {
+  const uint32_t have = row_blocks[r];
+  const uint32_t need = (target_tokens[r] + (uint32_t)block_size - 1) / (uint32_t)block_size;
+  return need > have && need <= (uint32_t)cols ? need - have : 0u;
+}
+
+__global__ __launch_bounds__(kMetaThreads) void allocate_rows_kernel(
     uint32_t* __restrict__ block_tables, int32_t cols, uint32_t* __restrict__ row_blocks,
     const uint32_t* __restrict__ target_tokens, uint8_t* __restrict__ ok,
     uint32_t* __restrict__ ring, uint32_t* __restrict__ ring_state, int32_t ring_cap,
     int32_t block_size, int32_t num_rows) {
-  if (threadIdx.x != 0) return;
-  uint32_t head = ring_state[0], avail = ring_state[1];
+  __shared__ uint32_t s_tmp[kMetaThreads / 64 + 1];
+  const int tid = threadIdx.x;
+  const uint32_t head0 = ring_state[0], avail0 = ring_state[1];
+  uint64_t total = 0;  // blocks all rows lack
+  for (int base = 0; base < num_rows; base += kMetaThreads) {
+    const int r = base + tid;
+    const uint32_t more =
+        r < num_rows ? blocks_missing(target_tokens, row_blocks, r, block_size, cols) : 0u;
+    uint32_t chunk;
+    block_exclusive_scan(more, s_tmp, &chunk);
+    total += chunk;
+  }
+  if (total <= avail0) {  // uniform: every row gets its blocks
+    uint32_t used = 0;
+    for (int base = 0; base < num_rows; base += kMetaThreads) {
+      const int r = base + tid;
+      uint32_t more = 0, need = 0, have = 0;
+      if (r < num_rows) {
+        have = row_blocks[r];
+        need = (target_tokens[r] + (uint32_t)block_size - 1) / (uint32_t)block_size;
+        more = need > have && need <= (uint32_t)cols ? need - have : 0u;
+      }
+      uint32_t chunk;
+      const uint32_t rank = block_exclusive_scan(more, s_tmp, &chunk);
+      if (r < num_rows) {
+        for (uint32_t i = 0; i < more; ++i)
+          block_tables[(int64_t)r * cols + have + i] =
+              ring[(head0 + used + rank + i) % (uint32_t)ring_cap];
+        if (more > 0) row_blocks[r] = need;
+        ok[r] = need <= (uint32_t)cols || need <= have ? 1 : 0;
+      }
+      used += chunk;
+    }
+    if (tid == 0) {
+      ring_state[0] = (uint32_t)((head0 + total) % (uint32_t)ring_cap);
+      ring_state[1] = avail0 - (uint32_t)total;
+    }
+    return;
+  }
+  if (tid != 0) return;
+  uint32_t head = head0, avail = avail0;
   for (int r = 0; r < num_rows; ++r) {
     const uint32_t have = row_blocks[r];
     const uint32_t need = (target_tokens[r] + (uint32_t)block_size - 1) / (uint32_t)block_size;
@@ -228,8 +279,8 @@ hipError_t launch_allocate_rows(uint32_t* block_tables, int32_t cols, uint32_t* 
                                 const uint32_t* target_tokens, uint8_t* ok, uint32_t* ring,
                                 uint32_t* ring_state, int32_t ring_cap, int32_t block_size,
                                 int32_t num_rows, hipStream_t stream) {
-  hipLaunchKernelGGL(allocate_rows_kernel, dim3(1), dim3(64), 0, stream, block_tables, cols,
-                     row_blocks, target_tokens, ok, ring, ring_state, ring_cap, block_size,
+  hipLaunchKernelGGL(allocate_rows_kernel, dim3(1), dim3(kMetaThreads), 0, stream, block_tables,
+                     cols, row_blocks, target_tokens, ok, ring, ring_state, ring_cap, block_size,
                      num_rows);
   return hipGetLastError();
 }

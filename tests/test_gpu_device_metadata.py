@@ -115,3 +115,29 @@ def test_device_allocator_follows_host_block_manager(device, graph):
         torch.cuda.synchronize()
         check_same(alloc, mgr, rids, f"release {step}")
     assert stalls_seen > 0, "the pool never ran dry: the stall path was not exercised"
+
+
+def test_admission_fits_then_overflows(device):
+    """A first admission whose missing blocks all fit the ring (every row
+    takes its blocks at once) and a second, growing the same rows, that does
+    not (rows are served in order until the ring runs dry, later rows that
+    still fit succeed): tables, counts and ok flags equal the host block
+    manager's after each. (The host manager has no table width, so rows are
+    kept within the device tables' columns.)"""
+    rng = np.random.default_rng(21)
+    num_blocks, bs, batch, cols = 130, 16, 40, 12
+    mgr = host.BlockManager(num_blocks, bs)
+    alloc = vpa.DeviceBlockAllocator(num_blocks, bs, batch, cols, device)
+    rids = list(range(batch))
+    first = rng.integers(1, 50, size=batch)
+    second = np.minimum(first + rng.integers(0, 120, size=batch), cols * bs)
+    for round_, target in enumerate((first, second)):
+        ok_host = [mgr.try_allocate_slots(rid, int(t)) for rid, t in zip(rids, target)]
+        ok_dev = alloc.allocate(u32(target, device)).cpu().numpy().astype(bool)
+        torch.cuda.synchronize()
+        assert ok_dev.tolist() == ok_host, f"round {round_}"
+        check_same(alloc, mgr, rids, f"round {round_}")
+        if round_ == 0:
+            assert all(ok_host), "the first admission should fit"
+        else:
+            assert not all(ok_host) and any(ok_host[6:]), "want failures and later successes"
