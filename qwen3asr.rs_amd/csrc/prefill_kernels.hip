@@ -28,12 +28,16 @@
 // type for the MFMA; the row sums use the unrounded values. The output is
 // acc / sum without an epsilon, as flash attention computes it.
 //
-// Tile pipeline: K and V tiles travel HBM -> LDS by the LDS-DMA form of the
-// 16-byte global load (no VGPR round trip) into kPrefillStages stage
-// buffers; tile t + stages - 1 is issued while tile t is consumed, waits are
-// explicit vmcnt counts plus a bare workgroup barrier (the compiler's
-// __syncthreads would drain every outstanding DMA), and the operand reads
-// from LDS are written as ds_read with their own lgkmcnt wait so the
+// Tile pipeline: a pipeline step is kPrefillSub tiles (two: one barrier,
+// one max exchange and one rescale test per 64 keys, which the fp8 path,
+// with its operand conversions, needs most; both cache types use the same
+// steps, so their rescale points, and with scales 1 their results, agree).
+// K and V tiles travel HBM -> LDS by the LDS-DMA form of the 16-byte global
+// load (no VGPR round trip) into kPrefillStages stage buffers; step
+// t + stages - 1 is issued while step t is consumed, waits are explicit
+// vmcnt counts plus a bare workgroup barrier (the compiler's __syncthreads
+// would drain every outstanding DMA), and the operand reads from LDS are
+// written as ds_read with their own lgkmcnt wait so the
 // compiler does not add a full vmcnt drain before them. Each DMA copies 64
 // units of one cache block, so its address is a scalar block base plus a
 // fixed per-lane offset. In LDS, K keeps the block's [chunk][key] order and
@@ -43,7 +47,7 @@
 // gfx950's 64 four-byte banks).
 //
 // Softmax: scores are in log2 units (scale * log2 e folded into the scale);
-// the running max only moves when a tile's max exceeds it by more than
+// the running max only moves when a step's max exceeds it by more than
 // kRescaleSlack, so O and the row sums are rescaled rarely and the
 // probabilities stay below 2^kRescaleSlack; the result is the same
 // sum(p v) / sum(p) for any choice of the reference max.
@@ -84,13 +88,18 @@ __device__ __forceinline__ float max_xor32(float v) {
 }
 
 #ifndef VPA_PREFILL_STAGES
-#define VPA_PREFILL_STAGES 4
+#define VPA_PREFILL_STAGES 2
 #endif
 #ifndef VPA_PREFILL_WAVES_PER_EU
 #define VPA_PREFILL_WAVES_PER_EU 2
 #endif
+#ifndef VPA_PREFILL_SUB
+#define VPA_PREFILL_SUB 2
+#endif
 constexpr int kPrefillKeys = 32;                    // keys per tile
-constexpr int kPrefillStages = VPA_PREFILL_STAGES;  // LDS tile buffers (tiles in flight + 1)
+constexpr int kPrefillSub = VPA_PREFILL_SUB;        // tiles per pipeline step
+constexpr int kPrefillStages = VPA_PREFILL_STAGES;  // LDS step buffers (steps in flight + 1)
+static_assert(kPrefillSub == 1 || kPrefillSub == 2, "tiles per step");
 #ifndef VPA_PREFILL_WAVES
 #define VPA_PREFILL_WAVES 4
 #endif
@@ -212,6 +221,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   static_assert(kF8 || std::is_same_v<C, T>, "cache type is the query type or fp8");
   constexpr int KT = kPrefillKeys;
   constexpr int NS = kPrefillStages;
+  constexpr int SUB = kPrefillSub;
   constexpr int X = kF8 ? 16 : 8;  // cache elements per 16-byte unit
   constexpr int PPW = 32 / G;   // query positions per wave
   constexpr int PPB = kPrefillWaves * PPW;  // query positions per workgroup
@@ -236,8 +246,10 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
 
   // one LDS object per stage: the compiler then knows that a DMA into one
   // stage does not alias the operand reads of another.
-  // stage buffer: K regions [block][chunk][key], then V regions [block][unit][dim]
-  __shared__ __align__(16) uint4 s_t0[KU + NU], s_t1[KU + NU], s_t2[KU + NU], s_t3[KU + NU];
+  // stage buffer: SUB tiles, each K regions [block][chunk][key], then V
+  // regions [block][unit][dim]
+  constexpr int TU = KU + NU;  // units of one tile in a stage
+  __shared__ __align__(16) uint4 s_t0[SUB * TU], s_t1[SUB * TU], s_t2[SUB * TU], s_t3[SUB * TU];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -262,6 +274,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   const int wg_end = min(p0 + PPB, q_len);
   const int n_keys = max(0, causal ? min(k_len, wg_end + shift) : k_len);
   const int n_tiles = (n_keys + KT - 1) / KT;
+  const int n_steps = (n_tiles + SUB - 1) / SUB;
 
   // this lane's query row (column of S^T and O^T)
   const int col = lane & 31;
@@ -317,14 +330,15 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   const uint32_t* bt = block_tables + (int64_t)s * block_table_stride;
   const int last_blk = max(k_len - 1, 0) / BS;
 
-  auto kst = [&](auto sc) -> uint4* {
+  // K and V regions of tile u of stage S
+  auto kst = [&](auto sc, int u) -> uint4* {
     constexpr int S = decltype(sc)::value;
-    if constexpr (S == 0) return s_t0;
-    else if constexpr (S == 1) return s_t1;
-    else if constexpr (S == 2) return s_t2;
-    else return s_t3;
+    if constexpr (S == 0) return s_t0 + u * TU;
+    else if constexpr (S == 1) return s_t1 + u * TU;
+    else if constexpr (S == 2) return s_t2 + u * TU;
+    else return s_t3 + u * TU;
   };
-  auto vst = [&](auto sc) -> uint4* { return kst(sc) + KU; };
+  auto vst = [&](auto sc, int u) -> uint4* { return kst(sc, u) + KU; };
   // block ids of a tile (uniform: scalar loads; the index is clamped to the
   // sequence's last block, which exists whenever a tile is touched)
   auto tile_blocks = [&](int k0, uint32_t (&pb)[NBT]) {
@@ -344,29 +358,33 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     voff[i] = (uint32_t)((r % D) * BS + (r / D) * X);
   }
 
-  // Issue the DMAs of tile t into stage S. Keys past the context and absent
-  // blocks read block 0 (in bounds); they are masked in S and their values
-  // zeroed when the V operands are built.
+  // Issue the DMAs of the SUB tiles of step t into stage S (always all SUB
+  // of them, so every step moves the same count). Keys past the context and
+  // absent blocks read block 0 (in bounds); they are masked in S and their
+  // values zeroed when the V operands are built.
   auto issue = [&](auto sc, int t) {
     if (DMW < kPrefillWaves && wave >= DMW) return;  // wave issues no DMA (uniform)
-    const int k0 = t * KT;
-    uint32_t pb[NBT];
-    tile_blocks(k0, pb);
-    uint4* sk = kst(sc);
-    uint4* sv = vst(sc);
 #pragma unroll
-    for (int i = 0; i < DPW; ++i) {
-      const int di = wave * DPW + i;  // uniform
-      const int b = di / DPB;
-      uint32_t phys = pb[0];
+    for (int u = 0; u < SUB; ++u) {
+      const int k0 = (t * SUB + u) * KT;
+      uint32_t pb[NBT];
+      tile_blocks(k0, pb);
+      uint4* sk = kst(sc, u);
+      uint4* sv = vst(sc, u);
 #pragma unroll
-      for (int k = 1; k < NBT; ++k)
-        if (b == k) phys = pb[k];
-      phys = (k0 + b * BS < k_len && (int64_t)phys < num_blocks) ? phys : 0u;
-      phys = __builtin_amdgcn_readfirstlane(phys);
-      const int64_t blk = (int64_t)phys * block_stride;
-      dma16(kbase + blk + koff[i], sk + b * RBK + (di % DPB) * 64);
-      dma16(vbase + blk + voff[i], sv + b * RBV + (di % DPB) * 64);
+      for (int i = 0; i < DPW; ++i) {
+        const int di = wave * DPW + i;  // uniform
+        const int b = di / DPB;
+        uint32_t phys = pb[0];
+#pragma unroll
+        for (int k = 1; k < NBT; ++k)
+          if (b == k) phys = pb[k];
+        phys = (k0 + b * BS < k_len && (int64_t)phys < num_blocks) ? phys : 0u;
+        phys = __builtin_amdgcn_readfirstlane(phys);
+        const int64_t blk = (int64_t)phys * block_stride;
+        dma16(kbase + blk + koff[i], sk + b * RBK + (di % DPB) * 64);
+        dma16(vbase + blk + voff[i], sv + b * RBV + (di % DPB) * 64);
+      }
     }
   };
 
@@ -407,9 +425,9 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   // Zero the LDS values of the keys vmask leaves out: their slots hold
   // stale data (maybe NaN), and a zero probability times NaN would poison O.
   // Element k % X of unit (k / X, d) holds key k of dim d.
-  auto zero_absent_values = [&](auto sc, uint32_t vmask) {
+  auto zero_absent_values = [&](uint4* sv, uint32_t vmask) {
     using E = std::conditional_t<kF8, uint8_t, uint16_t>;
-    E* ve = reinterpret_cast<E*>(vst(sc));
+    E* ve = reinterpret_cast<E*>(sv);
     const uint32_t absent = ~vmask;
     for (int e = tid; e < KT * D; e += kPrefillThreads) {
       const int k = e / D, d = e % D;
@@ -417,11 +435,9 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     }
   };
 
-  auto compute = [&](auto sc, int t, uint32_t vmask) {
-    const int k0 = t * KT;
-    if (k0 >= wave_keys) return;  // no row of this wave sees these keys
-    const uint4* sk = kst(sc);
-    const uint4* sv = vst(sc);
+  // S^T of one tile (keys k0 .. k0 + 31) with the keys this lane's row does
+  // not see at -inf
+  auto scores = [&](const uint4* sk, int k0, uint32_t vmask) -> f32x16_t {
     const bool full = vmask == 0xffffffffu && k0 + KT - 1 <= wave_min_limit;
 
     // S^T = K . Q^T; the K operand of k-step ks is chunk 2 ks + half of the
@@ -448,9 +464,6 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
                    "+v"(kop[3]));
     }
     f32x16_t sacc = s_tile_mfma<T, KS>(kop, qop);
-
-    // online softmax of the row on the raw scores (the scale is positive);
-    // P^T operands straight from the accumulator
     if (!full) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -459,25 +472,12 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
         sacc[r] = ok ? sacc[r] : -INFINITY;
       }
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
-    mx = max_xor32(mx) * sl;
-    // The reference max m only moves when some row's tile max exceeds it by
-    // more than kRescaleSlack (log2 units): the probabilities stay below
-    // 2^kRescaleSlack, and O and the row sums are rescaled only then.
-    constexpr float kRescaleSlack = 8.f;
-    if (__ballot(mx > m + kRescaleSlack) != 0) {
-      const float m_new = fmaxf(m, mx);
-      const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
-      lsum *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-      m = m_new;
-    }
-    const float m_use = m == -INFINITY ? 0.f : m;  // a row without keys so far
+    return sacc;
+  };
+
+  // probabilities of one tile against the reference max, added to the row
+  // sum; O^T += V^T . P^T with P^T straight from the accumulator
+  auto accumulate = [&](const uint4* sv, const f32x16_t& sacc, float m_use) {
     float sval[16];
     float ps = 0.f;
 #pragma unroll
@@ -493,9 +493,9 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
                           pack2_hw<T>(sval[8 * k2 + 2], sval[8 * k2 + 3]),
                           pack2_hw<T>(sval[8 * k2 + 4], sval[8 * k2 + 5]),
                           pack2_hw<T>(sval[8 * k2 + 6], sval[8 * k2 + 7]));
-    // O^T += V^T . P^T: k-step k2 of lane half h covers keys 16 k2 + 8h ..
-    // 16 k2 + 8h + 7, one unit of row d = 32 dt + col (values of absent keys
-    // were zeroed in LDS by the step)
+    // k-step k2 of lane half h covers keys 16 k2 + 8h .. 16 k2 + 8h + 7, one
+    // unit of row d = 32 dt + col (values of absent keys were zeroed in LDS
+    // by the step)
     v4i_t vop[DT][2];
     if constexpr (kF8) {
       v2i_t v8[DT][2];
@@ -528,37 +528,90 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
         o[dt] = mfma32x32x16<T>(__builtin_bit_cast(uint4, vop[dt][k2]), pk[k2], o[dt]);
   };
 
-  // one pipeline step: wait for tile t, refill the stage tile t-1 used with
-  // tile t + NS - 1, compute tile t
+  // the SUB tiles of step t: scores of each, one online-softmax update for
+  // the step (on the raw scores; the scale is positive), then P.V of each
+  auto compute = [&](auto sc, int t, const uint32_t (&vmask)[SUB]) {
+    const int k0 = t * SUB * KT;
+    if (k0 >= wave_keys) return;  // no row of this wave sees these keys
+    f32x16_t sacc[SUB];
+    sacc[0] = scores(kst(sc, 0), k0, vmask[0]);
+    if constexpr (SUB == 2) {
+      if (k0 + KT < wave_keys) {
+        sacc[1] = scores(kst(sc, 1), k0 + KT, vmask[1]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[1][r] = -INFINITY;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < SUB; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
+    mx = max_xor32(mx) * sl;
+    // The reference max m only moves when some row's step max exceeds it by
+    // more than kRescaleSlack (log2 units): the probabilities stay below
+    // 2^kRescaleSlack, and O and the row sums are rescaled only then.
+    constexpr float kRescaleSlack = 8.f;
+    if (__ballot(mx > m + kRescaleSlack) != 0) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+      m = m_new;
+    }
+    const float m_use = m == -INFINITY ? 0.f : m;  // a row without keys so far
+    accumulate(vst(sc, 0), sacc[0], m_use);
+    if constexpr (SUB == 2) {
+      if (k0 + KT < wave_keys) accumulate(vst(sc, 1), sacc[1], m_use);
+    }
+  };
+
+  // one pipeline step: wait for step t's tiles, refill the stage step t-1
+  // used with step t + NS - 1, compute step t
   auto step = [&](auto sc, int t) {
-    if (t >= n_tiles) return;
+    if (t >= n_steps) return;
     constexpr int S = decltype(sc)::value;
-    const int after = min(NS - 2, n_tiles - 1 - t);  // later tiles already issued
-    if (after >= 2) wait_vmcnt<2 * DPT>();
-    else if (after == 1) wait_vmcnt<DPT>();
+    constexpr int DPS = DPT * SUB;  // DMAs per wave per step
+    const int after = min(NS - 2, n_steps - 1 - t);  // later steps already issued
+    if (after >= 2) wait_vmcnt<2 * DPS>();
+    else if (after == 1) wait_vmcnt<DPS>();
     else wait_vmcnt<0>();
-    // tile t is in LDS for every wave, and every wave is done with tile t-1.
+    // step t is in LDS for every wave, and every wave is done with step t-1.
     // A bare s_barrier: __syncthreads() would also fence this wave's LDS
-    // writes, i.e. wait for all of its outstanding DMAs, later tiles
-    // included; the explicit vmcnt wait above already covers tile t.
+    // writes, i.e. wait for all of its outstanding DMAs, later steps
+    // included; the explicit vmcnt wait above already covers step t.
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    const uint32_t vmask = tile_mask(t);
-    if (vmask != 0xffffffffu) {  // rare: the sequence's last tile, absent blocks
-      zero_absent_values(sc, vmask);
+    uint32_t vmask[SUB];
+    bool fix = false;
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) {
+      vmask[u] = tile_mask(t * SUB + u);
+      // tiles past the last one are read by no wave
+      fix |= vmask[u] != 0xffffffffu && t * SUB + u < n_tiles;
+    }
+    if (fix) {  // rare: the sequence's last tile, absent blocks
+#pragma unroll
+      for (int u = 0; u < SUB; ++u)
+        if (vmask[u] != 0xffffffffu && t * SUB + u < n_tiles)
+          zero_absent_values(vst(sc, u), vmask[u]);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     }
-    if (t + NS - 1 < n_tiles) issue(Int<(S + NS - 1) % NS>{}, t + NS - 1);
+    if (t + NS - 1 < n_steps) issue(Int<(S + NS - 1) % NS>{}, t + NS - 1);
     compute(sc, t, vmask);
   };
-  if (n_tiles > 0) {
+  if (n_steps > 0) {
     issue(Int<0>{}, 0);
-    if (NS > 2 && 1 < n_tiles) issue(Int<1 % NS>{}, 1);
-    if (NS > 3 && 2 < n_tiles) issue(Int<2 % NS>{}, 2);
-    for (int t0 = 0; t0 < n_tiles; t0 += NS) {
+    if (NS > 2 && 1 < n_steps) issue(Int<1 % NS>{}, 1);
+    if (NS > 3 && 2 < n_steps) issue(Int<2 % NS>{}, 2);
+    for (int t0 = 0; t0 < n_steps; t0 += NS) {
       step(Int<0>{}, t0);
       step(Int<1 % NS>{}, t0 + 1);
       if constexpr (NS > 2) step(Int<2 % NS>{}, t0 + 2);
