@@ -407,6 +407,9 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(
 #ifndef VPA_DECODE_MERGE_WAVES_PER_CU
 #define VPA_DECODE_MERGE_WAVES_PER_CU 16
 #endif
+#ifndef VPA_DECODE_NV
+#define VPA_DECODE_NV 8
+#endif
 #ifndef VPA_DECODE_FP8_NV
 #define VPA_DECODE_FP8_NV 4
 #endif
@@ -468,8 +471,10 @@ void paged_decode_rows_kernel(
   // over its 64 / BS lanes with DPP / permlane swaps. A V stage reads BKS
   // value tiles the same way (lane l: row l / (BS/8) + k * 64 / (BS/8),
   // tokens (l % (BS/8)) * 8 .. +7).
-  constexpr int NV = kF8 ? VPA_DECODE_FP8_NV : 8;  // 16-byte loads per lane per stage
   constexpr int KPL = D * BS / (X * 64);  // loads per lane per tile (K or V)
+  // 16-byte loads per lane per stage (at least one tile)
+  constexpr int NV0 = kF8 ? VPA_DECODE_FP8_NV : VPA_DECODE_NV;
+  constexpr int NV = NV0 > KPL ? NV0 : KPL;
   constexpr int LPT = 64 / BS;            // lanes per token in a key tile
   constexpr int BKS = NV / KPL;           // tiles per stage
   static_assert(KPL == NVV && KPL >= 1 && KPL <= NV && NV % KPL == 0, "stage shape");
