@@ -94,7 +94,9 @@ int vpa_cache_layout(int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
  * bf16) k_scale and v_scale are device pointers to one f32 each and every
  * element is stored as E4M3FN(x / scale), rounded to nearest even and
  * saturated to +-448 (NaN stays NaN) — the rule of the fp8 caches of the
- * reference's paged-attention crate. num_tokens == 0 is a no-op.
+ * reference's paged-attention crate. num_tokens == 0 is a no-op; one call
+ * takes at most ceil(num_tokens / block_size) * num_kv_heads < 2^24
+ * (VPA_ERR_INVALID_ARGUMENT beyond: split the call).
  *
  * Cache strides: cache_block_stride / cache_head_stride are the element
  * strides of the first two dims of both caches (a (block, head) tile is

@@ -220,8 +220,11 @@ int vpa_reshape_and_cache(const void* key, const void* value, int64_t key_token_
   if (!aligned16(key) || !aligned16(value) || (key_token_stride * eb) % 16 != 0 ||
       (value_token_stride * eb) % 16 != 0)
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: key/value rows must be 16-byte aligned", op);
-  if ((num_tokens + block_size - 1) / block_size > 0x7fffffffLL)
-    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: too many tokens: %lld", op, (long long)num_tokens);
+  // one 256-lane workgroup per (group of block_size tokens, kv head) on a 1D
+  // grid, whose lane count must fit in 32 bits
+  if ((num_tokens + block_size - 1) / block_size * num_kv_heads > 0xffffffLL)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: too many tokens for one launch: %lld", op,
+                (long long)num_tokens);
   CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
               cache_head_stride};
   return hip_status(op, launch_reshape_and_cache(dtype, cache_dtype, key, value,

@@ -31,6 +31,9 @@ namespace vpa {
 namespace {
 
 constexpr int kThreads = 256;
+#ifndef VPA_APPEND_HEAD_FAST
+#define VPA_APPEND_HEAD_FAST 1
+#endif
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -74,7 +77,7 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
     int64_t value_token_stride, C* __restrict__ key_cache, C* __restrict__ value_cache,
     const int64_t* __restrict__ slot_mapping, int64_t num_tokens, int64_t num_slots,
     int64_t block_stride, int64_t head_stride, const float* __restrict__ k_scale,
-    const float* __restrict__ v_scale) {
+    const float* __restrict__ v_scale, int32_t num_kv_heads) {
   constexpr bool kQuant = !std::is_same_v<T, C>;
   static_assert(!kQuant || std::is_same_v<C, fp8_t>, "a cache type differing from the rows is fp8");
   constexpr int X = pack_x<C>();
@@ -88,8 +91,16 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
   __shared__ int64_t slots[BS];
 
   const int tid = threadIdx.x;
+#if VPA_APPEND_HEAD_FAST
+  // kv heads vary fastest over the grid: consecutive workgroups read the
+  // adjacent head slices of the same token rows and write the adjacent head
+  // tiles of the same cache block
+  const int head = (int)(blockIdx.x % (uint32_t)num_kv_heads);
+  const int64_t t0 = (int64_t)(blockIdx.x / (uint32_t)num_kv_heads) * BS;
+#else
   const int head = blockIdx.y;
   const int64_t t0 = (int64_t)blockIdx.x * BS;
+#endif
 
   if (tid < BS) {
     const int64_t t = t0 + tid;
@@ -403,11 +414,16 @@ hipError_t launch_rc_t(const void* key, const void* value, int64_t kts, int64_t 
                        void* vc, const int64_t* slots, int64_t num_tokens, const CacheGeom& g,
                        const float* k_scale, const float* v_scale, hipStream_t stream) {
   const int64_t groups = (num_tokens + BS - 1) / BS;
+#if VPA_APPEND_HEAD_FAST
+  dim3 grid((unsigned)(groups * g.num_kv_heads));
+#else
   dim3 grid((unsigned)groups, (unsigned)g.num_kv_heads);
+#endif
   hipLaunchKernelGGL((reshape_and_cache_kernel<T, C, D, BS>), grid, dim3(kThreads), 0, stream,
                      static_cast<const T*>(key), static_cast<const T*>(value), kts, vts,
                      static_cast<C*>(kc), static_cast<C*>(vc), slots, num_tokens,
-                     g.num_blocks * (int64_t)BS, g.block_stride, g.head_stride, k_scale, v_scale);
+                     g.num_blocks * (int64_t)BS, g.block_stride, g.head_stride, k_scale, v_scale,
+                     (int32_t)g.num_kv_heads);
   return hipGetLastError();
 }
 template <typename T, int D, int BS>

@@ -95,6 +95,8 @@ def rc_call(**over):
     (dict(key=FAKE + 2), _lib.VPA_ERR_INVALID_ARGUMENT, "aligned"),
     (dict(t=-1), _lib.VPA_ERR_INVALID_ARGUMENT, "num_tokens"),
     (dict(nb=0), _lib.VPA_ERR_INVALID_ARGUMENT, "positive"),
+    # one launch: groups of 16 tokens x 8 kv heads must stay below 2^24
+    (dict(t=16 * (1 << 24) // 8), _lib.VPA_ERR_INVALID_ARGUMENT, "too many tokens"),
 ])
 def test_reshape_and_cache_host_validation(over, code, needle):
     rc, msg = rc_call(**over)
