@@ -210,6 +210,7 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
  * cache_dtype (bit-exact copy), or the cache is VPA_DTYPE_FP8_E4M3 and
  * out_dtype f32 / f16 / bf16: each value is (float)byte * scale rounded to
  * nearest even, with k_scale / v_scale device pointers to one f32 each.
+ * num_seqs and block_table_stride are at most 65535 (VPA_ERR_UNSUPPORTED).
  */
 int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
                         const void* value_cache, const float* k_scale, const float* v_scale,

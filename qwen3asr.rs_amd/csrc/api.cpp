@@ -441,8 +441,10 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
                 "%s: bad sizes num_seqs=%d total_tokens=%lld block_table_stride=%d", op, num_seqs,
                 (long long)total_tokens, block_table_stride);
   if (num_seqs == 0 || total_tokens == 0 || block_table_stride == 0) return VPA_OK;
-  if (num_seqs > 65535)
-    return fail(VPA_ERR_UNSUPPORTED, "%s: num_seqs=%d exceeds 65535", op, num_seqs);
+  if (num_seqs > 65535 || block_table_stride > 65535)
+    return fail(VPA_ERR_UNSUPPORTED,
+                "%s: num_seqs=%d and block_table_stride=%d must not exceed 65535", op, num_seqs,
+                block_table_stride);
   if (out_key == nullptr || out_value == nullptr || block_tables == nullptr ||
       cu_seqlens_kv == nullptr)
     return fail(VPA_ERR_INVALID_ARGUMENT,

@@ -34,6 +34,9 @@ constexpr int kThreads = 256;
 #ifndef VPA_APPEND_HEAD_FAST
 #define VPA_APPEND_HEAD_FAST 1
 #endif
+#ifndef VPA_GATHER_HEAD_FAST
+#define VPA_GATHER_HEAD_FAST 1
+#endif
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -215,9 +218,16 @@ __global__ __launch_bounds__(kThreads) void gather_kv_cache_kernel(
   __shared__ T v_tile[D * BS];
 
   const int tid = threadIdx.x;
+#if VPA_GATHER_HEAD_FAST
+  // kv heads fastest: consecutive workgroups read the adjacent head tiles of
+  // one block and write adjacent head slices of the same rows
+  const int head = blockIdx.x;
+  const int b = blockIdx.y;
+#else
   const int b = blockIdx.x;
-  const int s = blockIdx.y;
   const int head = blockIdx.z;
+#endif
+  const int s = VPA_GATHER_HEAD_FAST ? blockIdx.z : blockIdx.y;
   const uint32_t row0 = cu_seqlens[s];
   const int64_t kv_len = (int64_t)cu_seqlens[s + 1] - (int64_t)row0;
   const int64_t tok0 = (int64_t)b * BS;
@@ -344,9 +354,16 @@ __global__ __launch_bounds__(kThreads) void gather_kv_cache_fp8_kernel(
   __shared__ __align__(16) uint8_t v_tile[D * BS];
 
   const int tid = threadIdx.x;
+#if VPA_GATHER_HEAD_FAST
+  // kv heads fastest: consecutive workgroups read the adjacent head tiles of
+  // one block and write adjacent head slices of the same rows
+  const int head = blockIdx.x;
+  const int b = blockIdx.y;
+#else
   const int b = blockIdx.x;
-  const int s = blockIdx.y;
   const int head = blockIdx.z;
+#endif
+  const int s = VPA_GATHER_HEAD_FAST ? blockIdx.z : blockIdx.y;
   const uint32_t row0 = cu_seqlens[s];
   const int64_t kv_len = (int64_t)cu_seqlens[s + 1] - (int64_t)row0;
   const int64_t tok0 = (int64_t)b * BS;
@@ -401,7 +418,11 @@ hipError_t launch_gather_fp8(void* ok, void* ov, const void* kc, const void* vc,
                              const uint32_t* bt, int32_t bts, const uint32_t* cu,
                              int32_t num_seqs, const CacheGeom& g, const float* k_scale,
                              const float* v_scale, hipStream_t stream) {
+#if VPA_GATHER_HEAD_FAST
+  dim3 grid((unsigned)g.num_kv_heads, (unsigned)bts, (unsigned)num_seqs);
+#else
   dim3 grid((unsigned)bts, (unsigned)num_seqs, (unsigned)g.num_kv_heads);
+#endif
   hipLaunchKernelGGL((gather_kv_cache_fp8_kernel<TO, D, BS>), grid, dim3(kThreads), 0, stream,
                      static_cast<TO*>(ok), static_cast<TO*>(ov), static_cast<const fp8_t*>(kc),
                      static_cast<const fp8_t*>(vc), bt, bts, cu, g.num_blocks, g.block_stride,
@@ -441,7 +462,11 @@ template <typename T, int D, int BS>
 hipError_t launch_gather(void* ok, void* ov, const void* kc, const void* vc,
                          const uint32_t* bt, int32_t bts, const uint32_t* cu, int32_t num_seqs,
                          const CacheGeom& g, hipStream_t stream) {
+#if VPA_GATHER_HEAD_FAST
+  dim3 grid((unsigned)g.num_kv_heads, (unsigned)bts, (unsigned)num_seqs);
+#else
   dim3 grid((unsigned)bts, (unsigned)num_seqs, (unsigned)g.num_kv_heads);
+#endif
   hipLaunchKernelGGL((gather_kv_cache_kernel<T, D, BS>), grid, dim3(kThreads), 0, stream,
                      static_cast<T*>(ok), static_cast<T*>(ov), static_cast<const T*>(kc),
                      static_cast<const T*>(vc), bt, bts, cu, g.num_blocks, g.block_stride,

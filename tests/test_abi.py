@@ -164,6 +164,12 @@ def test_gather_host_validation():
                                  16, 100, 8 * 128 * 16, 128 * 16, _lib.DTYPE_BF16,
                                  _lib.DTYPE_BF16, None)
     assert rc == 0
+    # the grid's y (table column) and z (sequence) extents
+    for bts, ns in ((65536, 2), (4, 65536)):
+        rc = lib.vpa_gather_kv_cache(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, bts, FAKE, ns, 10,
+                                     8, 128, 16, 100, 8 * 128 * 16, 128 * 16, _lib.DTYPE_BF16,
+                                     _lib.DTYPE_BF16, None)
+        assert rc == _lib.VPA_ERR_UNSUPPORTED and "65535" in lib.vpa_last_error().decode()
 
 
 def pf_call(**over):
