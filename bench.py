@@ -416,9 +416,10 @@ def device_step(w, dev, reps, warmup):
 def prefill_c4(dev, reps=10):
     """Row a3 measured alongside the headline: c4 (64 sequences x 512 new
     tokens over 0..1024 prior tokens, bf16) append with reshape_and_cache,
-    then causal chunked-prefill attention over the paged cache, and the same
-    prefill over fp8 caches; HIP events around each op on the current
-    stream, after 2 untimed calls."""
+    then causal chunked-prefill attention over the paged cache, the same
+    prefill over fp8 caches, and gather_kv_cache of every sequence's whole
+    context to packed rows (the reference's step before its flash prefill);
+    HIP events around each op on the current stream, after 2 untimed calls."""
     import numpy as np
     import torch
 
@@ -468,8 +469,16 @@ def prefill_c4(dev, reps=10):
                                            causal=True, max_query_len=mq, max_context_len=mk,
                                            out=out8)
 
+    cu_kv = torch.from_numpy(np.concatenate([[0], np.cumsum(w.context_lens)]).astype(np.uint32)
+                             ).to(dev)
+    kv_tokens = int(w.context_lens.sum())
+
+    def gather():
+        vpa.gather_kv_cache(kc, vc, None, None, bt, cu_kv, bf, total_tokens=kv_tokens)
+
     res = {}
-    for name, fn in (("append", append), ("prefill", prefill), ("prefill_fp8", prefill_fp8)):
+    for name, fn in (("append", append), ("prefill", prefill), ("prefill_fp8", prefill_fp8),
+                     ("gather", gather)):
         for _ in range(2):
             fn()
         e0 = torch.cuda.Event(enable_timing=True)
@@ -482,6 +491,7 @@ def prefill_c4(dev, reps=10):
         torch.cuda.synchronize()
         res[name] = e0.elapsed_time(e1) * 1e3 / reps  # us per call
     app_bytes = 2 * tq * 2 * kvh * d * 2 + 8 * tq
+    gather_bytes = 2 * 2 * kv_tokens * kvh * d * 2  # read the K/V tiles, write the rows
     flops = w.flops()
     tflops = flops / (res["prefill"] * 1e-6) / 1e12
     return {
@@ -493,6 +503,9 @@ def prefill_c4(dev, reps=10):
         "prefill_tflops": round(tflops, 2),
         "prefill_fp8_cache_us": round(res["prefill_fp8"], 2),
         "prefill_fp8_cache_tflops": round(flops / (res["prefill_fp8"] * 1e-6) / 1e12, 2),
+        "gather_tokens": kv_tokens,
+        "gather_us": round(res["gather"], 2),
+        "gather_gbps": round(gather_bytes / (res["gather"] * 1e-6) / 1e9, 2),
         "roofline": {"kernel": "chunked_prefill_paged_attention", "bound": "mfma",
                      "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
