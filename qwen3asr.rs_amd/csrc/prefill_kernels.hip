@@ -362,13 +362,17 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   // of them, so every step moves the same count). Keys past the context and
   // absent blocks read block 0 (in bounds); they are masked in S and their
   // values zeroed when the V operands are built.
-  auto issue = [&](auto sc, int t) {
+  // block ids of the SUB tiles of step t
+  auto step_blocks = [&](int t, uint32_t (&pbs)[SUB][NBT]) {
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) tile_blocks((t * SUB + u) * KT, pbs[u]);
+  };
+  auto issue = [&](auto sc, int t, const uint32_t (&pbs)[SUB][NBT]) {
     if (DMW < kPrefillWaves && wave >= DMW) return;  // wave issues no DMA (uniform)
 #pragma unroll
     for (int u = 0; u < SUB; ++u) {
       const int k0 = (t * SUB + u) * KT;
-      uint32_t pb[NBT];
-      tile_blocks(k0, pb);
+      const uint32_t(&pb)[NBT] = pbs[u];
       uint4* sk = kst(sc, u);
       uint4* sv = vst(sc, u);
 #pragma unroll
@@ -408,10 +412,8 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
 
   // keys of tile t that exist: inside the context and in a present block
   // (uniform over the workgroup)
-  auto tile_mask = [&](int t) {
+  auto tile_mask = [&](int t, const uint32_t (&pb)[NBT]) {
     const int k0 = t * KT;
-    uint32_t pb[NBT];
-    tile_blocks(k0, pb);
     uint32_t vmask = 0;
 #pragma unroll
     for (int kb = 0; kb < NBT; ++kb)
@@ -576,6 +578,12 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     if (t >= n_steps) return;
     constexpr int S = decltype(sc)::value;
     constexpr int DPS = DPT * SUB;  // DMAs per wave per step
+    // block ids of this step (masks) and of the step issued below, loaded
+    // before the waits so that their latency hides behind them
+    const bool refill = t + NS - 1 < n_steps;
+    uint32_t pm[SUB][NBT], pi[SUB][NBT];
+    step_blocks(t, pm);
+    if (refill) step_blocks(t + NS - 1, pi);
     const int after = min(NS - 2, n_steps - 1 - t);  // later steps already issued
     if (after >= 2) wait_vmcnt<2 * DPS>();
     else if (after == 1) wait_vmcnt<DPS>();
@@ -591,7 +599,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     bool fix = false;
 #pragma unroll
     for (int u = 0; u < SUB; ++u) {
-      vmask[u] = tile_mask(t * SUB + u);
+      vmask[u] = tile_mask(t * SUB + u, pm[u]);
       // tiles past the last one are read by no wave
       fix |= vmask[u] != 0xffffffffu && t * SUB + u < n_tiles;
     }
@@ -604,13 +612,21 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     }
-    if (t + NS - 1 < n_steps) issue(Int<(S + NS - 1) % NS>{}, t + NS - 1);
+    if (refill) issue(Int<(S + NS - 1) % NS>{}, t + NS - 1, pi);
     compute(sc, t, vmask);
   };
   if (n_steps > 0) {
-    issue(Int<0>{}, 0);
-    if (NS > 2 && 1 < n_steps) issue(Int<1 % NS>{}, 1);
-    if (NS > 3 && 2 < n_steps) issue(Int<2 % NS>{}, 2);
+    uint32_t p0[SUB][NBT];
+    step_blocks(0, p0);
+    issue(Int<0>{}, 0, p0);
+    if (NS > 2 && 1 < n_steps) {
+      step_blocks(1, p0);
+      issue(Int<1 % NS>{}, 1, p0);
+    }
+    if (NS > 3 && 2 < n_steps) {
+      step_blocks(2, p0);
+      issue(Int<2 % NS>{}, 2, p0);
+    }
     for (int t0 = 0; t0 < n_steps; t0 += NS) {
       step(Int<0>{}, t0);
       step(Int<1 % NS>{}, t0 + 1);
