@@ -147,6 +147,22 @@ def test_prefill_invalid_block_ids_are_skipped(device):
     assert_attention_close(got, want, orc.BF16, "invalid blocks")
 
 
+@pytest.mark.parametrize("col", [2, 4, 7])
+def test_prefill_absent_block_in_either_tile_of_a_step(device, col):
+    """The kernel consumes keys in steps of two 32-key tiles. An absent block
+    (id past the pool) in the second tile of step 0 (column 2), the first
+    tile of step 1 (column 4) or the second tile of step 1 (column 7), over a
+    pool whose unused slots hold NaN (block 0, read in place of the absent
+    block, among them), must be masked and its values zeroed in whichever
+    tile it falls."""
+    def mutate(bt):
+        bt[0, col] = 1 << 30
+    got, want = prefill_case(device, orc.BF16, 16, 8, 128, 16, [100, 60], [40, 50],
+                             seed=16 + col, stale_nan=True, mutate_bt=mutate)
+    assert np.isfinite(got).all()
+    assert_attention_close(got, want, orc.BF16, f"absent column {col}")
+
+
 def test_prefill_padded_table_columns_and_frozen_maxima(device):
     """Extra zero columns in block_tables and host maxima above the true ones
     (a grid sized for a larger batch) change nothing."""
