@@ -287,6 +287,20 @@ def test_fp8_prefill_absent_blocks(device):
     assert_attention_close(got, want, orc.BF16, "fp8 prefill absent blocks")
 
 
+@pytest.mark.parametrize("col", [2, 4, 7])
+def test_fp8_prefill_absent_block_in_either_tile_of_a_step(device, col):
+    """An absent block in the second tile of step 0 (column 2), the first of
+    step 1 (column 4) or the second of step 1 (column 7) of the two-tile
+    steps; block 0, read in its place, holds NaN bytes in every slot no
+    sequence uses: its values must be zeroed bytewise in either tile."""
+    def mutate(bt):
+        bt[0, col] = 1 << 30
+    got, want, _ = fp8_prefill_case(device, orc.BF16, 16, 8, 16, [100, 60], [40, 50],
+                                    seed=40 + col, mutate_bt=mutate)
+    assert np.isfinite(got).all()
+    assert_attention_close(got, want, orc.BF16, f"fp8 prefill absent column {col}")
+
+
 def test_fp8_prefill_equals_bf16_prefill_over_dequantised_cache(device):
     """Scales 1: E4M3 values are exact in bf16, so the fp8 kernel feeds the
     MFMAs the same operands as the bf16 kernel over a bf16 copy of the cache
