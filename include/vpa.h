@@ -245,7 +245,7 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
  * max_kv_len, which size the grid only; rows at or past total_query_rows are
  * neither read nor written. Block ids >= num_blocks are treated as absent.
  * out[row, h] = sum_t p_t V[t] / sum_t p_t (no epsilon, as flash attention).
- * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 (head_dim 128,
+ * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 (head_dim 64 or 128,
  * block_size 16 or 32) for bf16/f16 queries: the cache is read as byte *
  * k_scale / byte * v_scale (the Metal kernel's fp8 path,
  * prefill_paged_attn.metal:698-769), converted to the query type in

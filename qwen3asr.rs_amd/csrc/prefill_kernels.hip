@@ -446,11 +446,15 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     // key in row col
     v4i_t kop[KS];
     if constexpr (kF8) {
-      static_assert(KS == 8, "fp8: head_dim 128");
       v2i_t k8[KS];
       lds_read_seq8<BS * 16>(k8, ka_lane + lds_addr(sk), std::make_integer_sequence<int, KS>{});
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k8[0]), "+v"(k8[1]), "+v"(k8[2]), "+v"(k8[3]),
-                   "+v"(k8[4]), "+v"(k8[5]), "+v"(k8[6]), "+v"(k8[7]));
+      if constexpr (KS == 8) {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k8[0]), "+v"(k8[1]), "+v"(k8[2]), "+v"(k8[3]),
+                     "+v"(k8[4]), "+v"(k8[5]), "+v"(k8[6]), "+v"(k8[7]));
+      } else {
+        static_assert(KS == 4, "head_dim 64 or 128");
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k8[0]), "+v"(k8[1]), "+v"(k8[2]), "+v"(k8[3]));
+      }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kop[ks] = fp8x8_operand<T>(k8[ks]);
     } else if constexpr (KS == 8) {
@@ -503,9 +507,15 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
       v2i_t v8[DT][2];
       lds_read_pairs8<32 * 16, kVStep1>(v8, va_lane + lds_addr(sv),
                                         std::make_integer_sequence<int, DT>{});
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(v8[0][0]), "+v"(v8[0][1]), "+v"(v8[1][0]), "+v"(v8[1][1]),
-                     "+v"(v8[2][0]), "+v"(v8[2][1]), "+v"(v8[3][0]), "+v"(v8[3][1]));
+      if constexpr (DT == 4) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(v8[0][0]), "+v"(v8[0][1]), "+v"(v8[1][0]), "+v"(v8[1][1]),
+                       "+v"(v8[2][0]), "+v"(v8[2][1]), "+v"(v8[3][0]), "+v"(v8[3][1]));
+      } else {
+        static_assert(DT == 2, "head_dim 64 or 128");
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(v8[0][0]), "+v"(v8[0][1]), "+v"(v8[1][0]), "+v"(v8[1][1]));
+      }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -714,12 +724,11 @@ hipError_t dispatch_shape(int group, const PrefillArgs& a, const CacheGeom& g,
     if constexpr (!kF8)
       if (g.block_size == 8) return dispatch_group<T, C, 128, 8>(group, a, g, stream);
   }
-  if constexpr (!kF8) {
-    if (g.head_dim == 64) {
+  if (g.head_dim == 64) {
+    if constexpr (!kF8)
       if (g.block_size == 8) return dispatch_group<T, C, 64, 8>(group, a, g, stream);
-      if (g.block_size == 16) return dispatch_group<T, C, 64, 16>(group, a, g, stream);
-      if (g.block_size == 32) return dispatch_group<T, C, 64, 32>(group, a, g, stream);
-    }
+    if (g.block_size == 16) return dispatch_group<T, C, 64, 16>(group, a, g, stream);
+    if (g.block_size == 32) return dispatch_group<T, C, 64, 32>(group, a, g, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -730,7 +739,8 @@ bool prefill_supported(int dtype, int cache_dtype, int head_dim, int block_size,
   if (!(dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) || !(group == 1 || group == 2 ||
                                                                 group == 4))
     return false;
-  if (cache_dtype == VPA_DTYPE_FP8_E4M3) return head_dim == 128 && (block_size == 16 || block_size == 32);
+  if (cache_dtype == VPA_DTYPE_FP8_E4M3)
+    return (head_dim == 64 || head_dim == 128) && (block_size == 16 || block_size == 32);
   return cache_dtype == dtype && (head_dim == 64 || head_dim == 128) &&
          (block_size == 8 || block_size == 16 || block_size == 32);
 }

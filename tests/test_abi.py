@@ -319,7 +319,5 @@ def test_gather_and_prefill_fp8_validation():
     assert rc == _lib.VPA_ERR_INVALID_ARGUMENT and "k_scale" in msg, msg
     rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, dtype=_lib.DTYPE_F32, **F8_STRIDES)
     assert rc == _lib.VPA_ERR_UNSUPPORTED and "differs" in msg, msg
-    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bstride=8 * 64 * 16, hstride=64 * 16)
-    assert rc == _lib.VPA_ERR_UNSUPPORTED and "no MFMA kernel" in msg, msg
     rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bstride=8 * 128 * 8, hstride=128 * 8)
     assert rc == _lib.VPA_ERR_UNSUPPORTED and "no MFMA kernel" in msg, msg

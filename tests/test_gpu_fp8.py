@@ -214,11 +214,10 @@ def test_fp8_append_then_decode_end_to_end(device):
 # ---- chunked prefill over an fp8 cache ----------------------------------------
 
 def fp8_prefill_case(device, code, h, kvh, bs, prior, qlens, seed, causal=True,
-                     scales=(1.0, 1.0), mutate_bt=None):
+                     scales=(1.0, 1.0), mutate_bt=None, d=128):
     """Random fp8 caches with NaN bytes (0x7F) in every slot no sequence
     holds; returns (kernel output as f32, fp64 oracle, inputs)."""
     rng = np.random.default_rng(seed)
-    d = 128
     ks, vs = scales
     prior = np.asarray(prior, dtype=np.int64)
     qlens = np.asarray(qlens, dtype=np.int64)
@@ -301,14 +300,24 @@ def test_fp8_prefill_absent_block_in_either_tile_of_a_step(device, col):
     assert_attention_close(got, want, orc.BF16, f"fp8 prefill absent column {col}")
 
 
-def test_fp8_prefill_equals_bf16_prefill_over_dequantised_cache(device):
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("bs", [16, 32])
+def test_fp8_prefill_head_dim_64(device, bs, causal):
+    got, want, _ = fp8_prefill_case(device, orc.BF16, 16, 8, bs, PF_PRIOR, PF_NEW,
+                                    seed=70 + bs + causal, causal=causal, d=64)
+    assert np.isfinite(got).all()
+    assert_attention_close(got, want, orc.BF16, f"fp8 prefill d=64 bs={bs} causal={causal}")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_fp8_prefill_equals_bf16_prefill_over_dequantised_cache(device, d):
     """Scales 1: E4M3 values are exact in bf16, so the fp8 kernel feeds the
     MFMAs the same operands as the bf16 kernel over a bf16 copy of the cache
     (re-packed from 16 to 8 elements per key vector): the outputs are equal
     bit for bit."""
     code, h, kvh, bs = orc.BF16, 16, 8, 16
     got, _, (q, kc, vc, bt, lens, cu, scale) = fp8_prefill_case(
-        device, code, h, kvh, bs, [0, 17, 500], [64, 33, 90], seed=21)
+        device, code, h, kvh, bs, [0, 17, 500], [64, 33, 90], seed=21, d=d)
     nb, _, c16, _, _ = kc.shape
     d = c16 * 16
     kf = orc.fp8_to_f32(kc).transpose(0, 1, 3, 2, 4).reshape(nb, kvh, bs, d)
