@@ -504,12 +504,17 @@ void paged_decode_rows_kernel(
   if (s >= num_seqs) return;
   const int L = clamp_context(item.y, max_ctx, cap_tokens);
   if (L <= 0) {
-    for (int i = threadIdx.x; i < G * D; i += 64 * NW)
-      store_from_f32<T>(out + ((int64_t)s * num_heads + j * G) * D + i, 0.f);
+    if (chunk == 0)
+      for (int i = threadIdx.x; i < G * D; i += 64 * NW)
+        store_from_f32<T>(out + ((int64_t)s * num_heads + j * G) * D + i, 0.f);
     return;
   }
   const int nblk = (L + BS - 1) / BS;
   const int nchunks = (nblk + PB * NW - 1) / (PB * NW);
+  // an item past the sequence's chunks (a list built for other lengths or
+  // another max_context_len) would write a partial row outside (s, h) or
+  // race with chunk 0 on the output: skip it
+  if (chunk >= nchunks || chunk >= max_parts) return;
   // the chunk's blocks are split evenly over the NW waves (at most PB each),
   // so short sequences keep every wave busy
   const int c_begin = chunk * PB * NW;
