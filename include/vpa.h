@@ -26,10 +26,14 @@
  *   - No entry point allocates device memory, synchronises, or reads device
  *     memory from the host, so every launch may be recorded into a HIP graph.
  *     Scratch memory comes from the caller (see
- *     vpa_paged_attention_workspace_size).
+ *     vpa_paged_attention_workspace_size), except for
+ *     vpa_paged_attention_noalloc, which uses a static device array of the
+ *     library.
  *   - `stream` is a hipStream_t (NULL = the null stream).
  *   - The library is reentrant; its only global state is the thread-local
- *     error message and a per-device cache of the compute-unit count.
+ *     error message, a per-device cache of the compute-unit count, and the
+ *     per-device decode scratch of vpa_paged_attention_noalloc with its
+ *     cached address.
  */
 #ifndef VPA_H_
 #define VPA_H_
@@ -195,6 +199,33 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
                                 int64_t cache_block_stride, int64_t cache_head_stride,
                                 int32_t dtype, int32_t cache_dtype, void* workspace,
                                 size_t workspace_bytes, void* stream);
+
+/*
+ * paged_attention_noalloc — vpa_paged_attention with no workspace argument
+ * and no allocation of any kind. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture
+ * that must not allocate, tight serving loops, harnesses that forbid
+ * hipMalloc). The split-K partials and the work list live in a static
+ * device array of the library, 64 MiB per GPU, held until the process ends
+ * and laid out for the kernel this configuration runs (16-bit / fp8 caches
+ * with head_dim <= 128: num_seqs * num_heads * ceil(max_context_len / 2048)
+ * partial rows of (head_dim + 32) floats, 5.3 MB at batch 256 / context
+ * 4096, 42 MB at batch 1024 / context 8192). A call whose layout does not
+ * fit returns VPA_ERR_WORKSPACE (after the other argument checks, before
+ * touching the device). Same arguments (minus the workspace), results and
+ * errors as vpa_paged_attention. Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (several streams or threads) race.
+ */
+int vpa_paged_attention_noalloc(void* out, const void* query, const float* k_scale,
+                                const float* v_scale, const void* key_cache,
+                                const void* value_cache, const uint32_t* block_tables,
+                                int32_t block_table_stride, const uint32_t* context_lens,
+                                const float* alibi_slopes, int32_t max_context_len,
+                                float softmax_scale, float softcapping, const float* sinks,
+                                int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                int64_t cache_block_stride, int64_t cache_head_stride,
+                                int32_t dtype, int32_t cache_dtype, void* stream);
 
 /*
  * gather_kv_cache — copy each sequence's first kv_len tokens out of the paged

@@ -241,9 +241,9 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
 
 }  // extern "C"
 
-namespace {
+namespace vpa {
 
-// paged_attention and its planned variant: all checks, then the launch.
+// paged_attention and its variants: all checks, then the launch.
 int paged_attention_impl(void* out, const void* query, const float* k_scale,
                          const float* v_scale, const void* key_cache,
                          const void* value_cache, const uint32_t* block_tables,
@@ -253,9 +253,9 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                          int32_t block_size, int64_t num_blocks, int64_t cache_block_stride,
                          int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
-                         void* workspace, size_t workspace_bytes, void* stream, bool planned) {
+                         void* workspace, size_t workspace_bytes, void* stream, bool planned,
+                         const DecodeScratch* scratch, const char* op) {
   clear_error();
-  const char* op = planned ? "paged_attention_planned" : "paged_attention";
   if (alibi_slopes != nullptr)
     return fail(VPA_ERR_UNSUPPORTED, "%s: alibi_slopes are not supported", op);
   if (sinks != nullptr) return fail(VPA_ERR_UNSUPPORTED, "%s: sinks are not supported", op);
@@ -314,7 +314,25 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
     return fail(VPA_ERR_INVALID_ARGUMENT,
                 "%s: block_table_stride=%d too small for max_context_len=%d (block_size=%d)", op,
                 block_table_stride, max_context_len, block_size);
-  const size_t need = decode_workspace_bytes(num_seqs, num_heads, head_dim, max_context_len);
+  const int part_tokens =
+      scratch != nullptr ? decode_part_tokens(dtype, head_dim) : kDecodeMinPartitionTokens;
+  const size_t need =
+      decode_workspace_bytes(num_seqs, num_heads, head_dim, max_context_len, part_tokens);
+  if (scratch != nullptr) {
+    if (need > scratch->bytes)
+      return fail(VPA_ERR_WORKSPACE,
+                  "%s: this call needs %zu bytes of decode scratch, the library's static "
+                  "scratch holds %zu (num_seqs=%d num_heads=%d head_dim=%d max_context_len=%d); "
+                  "use vpa_paged_attention with a caller workspace",
+                  op, need, scratch->bytes, num_seqs, num_heads, head_dim, max_context_len);
+    workspace = nullptr;
+    workspace_bytes = 0;
+    if (need > 0) {
+      const int rc_s = scratch->address(op, &workspace);
+      if (rc_s != VPA_OK) return rc_s;
+      workspace_bytes = scratch->bytes;
+    }
+  }
   if (need > 0) {
     if (workspace == nullptr || workspace_bytes < need)
       return fail(VPA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", op, need,
@@ -324,8 +342,8 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
   }
   CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
               cache_head_stride};
-  DecodeWorkspace ws =
-      carve_decode_workspace(workspace, num_seqs, num_heads, head_dim, max_context_len);
+  DecodeWorkspace ws = carve_decode_workspace(workspace, num_seqs, num_heads, head_dim,
+                                              max_context_len, part_tokens);
   ws.planned = planned;
   return hip_status(op, launch_paged_decode(dtype, cache_dtype, out, query, key_cache,
                                             value_cache, block_tables, block_table_stride,
@@ -334,7 +352,7 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
                                             static_cast<hipStream_t>(stream)));
 }
 
-}  // namespace
+}  // namespace vpa
 
 extern "C" {
 
@@ -353,7 +371,7 @@ int vpa_paged_attention(void* out, const void* query, const float* k_scale,
                               softmax_scale, softcapping, sinks, num_seqs, num_heads,
                               num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
                               cache_head_stride, dtype, cache_dtype, workspace, workspace_bytes,
-                              stream, false);
+                              stream, false, nullptr, "paged_attention");
 }
 
 int vpa_paged_attention_planned(void* out, const void* query, const float* k_scale,
@@ -372,7 +390,7 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
                               softmax_scale, softcapping, sinks, num_seqs, num_heads,
                               num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
                               cache_head_stride, dtype, cache_dtype, workspace, workspace_bytes,
-                              stream, true);
+                              stream, true, nullptr, "paged_attention_planned");
 }
 
 int vpa_paged_attention_plan(const uint32_t* context_lens, int32_t max_context_len,

@@ -1091,11 +1091,15 @@ struct WorkspacePlan {
   size_t part_out, part_stat, items, multi, queue, total;
   int max_parts;
 };
-WorkspacePlan plan_workspace(int num_seqs, int num_heads, int head_dim, int max_context_len) {
+// Pieces of the decode scratch for split-K partitions of part_tokens tokens
+// (the caller workspace uses the smallest partition any kernel takes, so its
+// size depends on the sizes only; the tight layout uses the partition of
+// the kernel a configuration runs).
+WorkspacePlan plan_workspace(int num_seqs, int num_heads, int head_dim, int max_context_len,
+                             int part_tokens) {
   auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
-  constexpr int kMin = kDecodeMinPartitionTokens;
   WorkspacePlan w{};
-  w.max_parts = (max_context_len + kMin - 1) / kMin;
+  w.max_parts = (max_context_len + part_tokens - 1) / part_tokens;
   const size_t rows = w.max_parts > 1 ? (size_t)num_seqs * (size_t)num_heads * (size_t)w.max_parts : 0;
   w.part_out = up(rows * (size_t)(head_dim + 32) * sizeof(float));
   w.part_stat = up(rows * sizeof(float));
@@ -1107,15 +1111,24 @@ WorkspacePlan plan_workspace(int num_seqs, int num_heads, int head_dim, int max_
 }
 }  // namespace
 
-size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len) {
-  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_context_len < 0) return 0;
-  return plan_workspace(num_seqs, num_heads, head_dim, max_context_len).total;
+int decode_part_tokens(int dtype, int head_dim) {
+  const bool rows = (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) && head_dim <= 128;
+  return rows ? kDecodeChunk : kPT;
+}
+
+size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len,
+                              int part_tokens) {
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_context_len < 0 ||
+      part_tokens <= 0)
+    return 0;
+  return plan_workspace(num_seqs, num_heads, head_dim, max_context_len, part_tokens).total;
 }
 
 DecodeWorkspace carve_decode_workspace(void* base, int num_seqs, int num_heads, int head_dim,
-                                       int max_context_len) {
+                                       int max_context_len, int part_tokens) {
   DecodeWorkspace ws{};
-  const WorkspacePlan w = plan_workspace(num_seqs, num_heads, head_dim, max_context_len);
+  const WorkspacePlan w =
+      plan_workspace(num_seqs, num_heads, head_dim, max_context_len, part_tokens);
   ws.max_parts = w.max_parts;
   char* p = static_cast<char*>(base);
   ws.part_out = reinterpret_cast<float*>(p);

@@ -1,0 +1,88 @@
+// paged_attention without a caller workspace: the split-K partials, the work
+// list and its header live in a static device array of this library (one
+// copy per GPU, held until the process ends), so the entry point allocates
+// nothing — for callers that cannot call hipMalloc (code under stream
+// capture that must not allocate, tight serving loops, harnesses that forbid
+// allocation).
+//
+// The array is laid out for the kernel the configuration runs (the rows
+// kernel's 2048-token chunks for 16-bit / fp8 caches with head_dim <= 128,
+// the generic kernel's 256-token partitions otherwise), which is smaller
+// than the caller workspace of vpa_paged_attention (sized for any kernel).
+// Nothing in it needs to start at zero: the plan launch rewrites the work
+// list and its header, and every partial row the merge reads is written by
+// the same call first. Every call on a GPU shares that GPU's array, so
+// calls that overlap on one GPU (two streams, two threads) race.
+
+#include <atomic>
+#include <mutex>
+
+#include "vpa_internal.h"
+
+namespace vpa {
+namespace {
+
+// 64 MiB: the rows-kernel layout of every BASELINE decode shape fits (c3:
+// 5.3 MB, c5 with batch 1024 and contexts up to 8192: 42 MB).
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+
+// The library's decode scratch. In host code `scratch` names a host-side
+// stand-in: its device address comes from hipGetSymbolAddress, per device.
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's copy of `scratch`, looked up once
+// per device with that device current.
+int scratch_address(const char* op, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(VPA_ERR_HIP, "%s: hipGetDevice failed: %s", op, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: device ordinal %d out of range", op, dev);
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr)
+        return fail(VPA_ERR_HIP, "%s: hipGetSymbolAddress of the decode scratch failed: %s", op,
+                    hipGetErrorString(e));
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return VPA_OK;
+}
+
+}  // namespace
+}  // namespace vpa
+
+using namespace vpa;
+
+extern "C" {
+
+int vpa_paged_attention_noalloc(void* out, const void* query, const float* k_scale,
+                                const float* v_scale, const void* key_cache,
+                                const void* value_cache, const uint32_t* block_tables,
+                                int32_t block_table_stride, const uint32_t* context_lens,
+                                const float* alibi_slopes, int32_t max_context_len,
+                                float softmax_scale, float softcapping, const float* sinks,
+                                int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                int64_t cache_block_stride, int64_t cache_head_stride,
+                                int32_t dtype, int32_t cache_dtype, void* stream) {
+  static const DecodeScratch kScratch{kScratchBytes, scratch_address};
+  return paged_attention_impl(out, query, k_scale, v_scale, key_cache, value_cache, block_tables,
+                              block_table_stride, context_lens, alibi_slopes, max_context_len,
+                              softmax_scale, softcapping, sinks, num_seqs, num_heads,
+                              num_kv_heads, head_dim, block_size, num_blocks,
+                              cache_block_stride, cache_head_stride, dtype, cache_dtype, nullptr,
+                              0, stream, false, &kScratch, "paged_attention_noalloc");
+}
+
+}  // extern "C"

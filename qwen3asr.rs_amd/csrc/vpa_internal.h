@@ -41,16 +41,50 @@ struct DecodeWorkspace {
   uint2* items;      // [num_seqs * max(1, max_parts)] work list {seq << 16 | partition, length}
   uint32_t* multi;   // [num_seqs] sequences with more than one partition
   uint32_t* queue;   // [3]: next work unit, number of items, number of multi entries
-  int max_parts;     // ceil(max_context_len / kDecodeMinPartitionTokens)
+  int max_parts;     // ceil(max_context_len / partition tokens of the layout)
   bool planned = false;  // the work list is already in the workspace (skip the plan launch)
 };
 
 // Compute units of the current device (cached per device).
 int device_cu_count();
 
-size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len);
+// The library's own decode scratch (the allocation-free entry point): its
+// size and the lookup of its address on the current device.
+struct DecodeScratch {
+  size_t bytes;
+  int (*address)(const char* op, void** out);
+};
+
+// vpa_paged_attention and its variants: every argument check, then the
+// launches. With `scratch` the workspace arguments are ignored: after the
+// checks the call takes the library's scratch, laid out for the kernel that
+// runs (decode_part_tokens), and fails with VPA_ERR_WORKSPACE when that
+// layout does not fit it.
+int paged_attention_impl(void* out, const void* query, const float* k_scale,
+                         const float* v_scale, const void* key_cache, const void* value_cache,
+                         const uint32_t* block_tables, int32_t block_table_stride,
+                         const uint32_t* context_lens, const float* alibi_slopes,
+                         int32_t max_context_len, float softmax_scale, float softcapping,
+                         const float* sinks, int32_t num_seqs, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                         int64_t num_blocks, int64_t cache_block_stride,
+                         int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
+                         void* workspace, size_t workspace_bytes, void* stream, bool planned,
+                         const DecodeScratch* scratch, const char* op);
+
+// Split-K partition (tokens) of the decode kernel that runs for a query
+// dtype and head_dim: the rows kernel's chunk, or the generic kernel's
+// partition.
+int decode_part_tokens(int dtype, int head_dim);
+// Decode scratch bytes and layout for partitions of part_tokens tokens; the
+// caller workspace of vpa_paged_attention uses kDecodeMinPartitionTokens
+// (valid for every kernel), the library's own scratch the running kernel's
+// partition (decode_part_tokens).
+size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len,
+                              int part_tokens = kDecodeMinPartitionTokens);
 DecodeWorkspace carve_decode_workspace(void* base, int num_seqs, int num_heads, int head_dim,
-                                       int max_context_len);
+                                       int max_context_len,
+                                       int part_tokens = kDecodeMinPartitionTokens);
 
 // Launchers return hipSuccess or the launch error. Arguments are validated by
 // the caller.

@@ -1,0 +1,106 @@
+"""vpa_paged_attention_noalloc (the allocation-free decode entry point, whose
+split-K scratch is a static device array of the library) against
+vpa_paged_attention with a caller workspace, both called through the C ABI
+on the same inputs: outputs equal bit for bit (the same kernels run; only
+the scratch layout differs), on two calls in a row, the second with a
+smaller batch and shorter contexts so that it runs over what the first left
+in the array. The second call is also checked against the fp64 oracle.
+Covered: the rows kernel with multi-chunk sequences (bf16, merge launch),
+the fp8-cache rows kernel, and the generic kernel (f32, 256-token
+partitions)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests._util import (assert_attention_close, block_tables_for, make_cache, random_words,
+                         to_dev, to_host, u32)
+from vpa import _lib
+
+pytestmark = pytest.mark.gpu
+
+H, KVH, D, BS = 16, 8, 128, 16
+
+
+def case(rng, code, lens, cache_code=None):
+    cache_code = code if cache_code is None else cache_code
+    nb = sum((int(L) + BS - 1) // BS for L in lens) + 8
+    if cache_code == orc.FP8:
+        kc = rng.integers(0, 256, size=(nb, KVH, D // 16, BS, 16), dtype=np.uint8)
+        vc = rng.integers(0, 256, size=(nb, KVH, D, BS), dtype=np.uint8)
+        for c in (kc, vc):
+            c[(c & 0x7F) == 0x7F] = 0x38  # no NaN codes
+    else:
+        kc, vc = make_cache(rng, nb, KVH, D, BS, cache_code)
+    bt = block_tables_for(rng, lens, nb, BS)
+    q = random_words(rng, (len(lens), H, D), code)
+    return dict(q=q, kc=kc, vc=vc, bt=bt, lens=np.asarray(lens, dtype=np.uint32), nb=nb)
+
+
+def dev_cache(a, cache_code, device):
+    if cache_code == orc.FP8:
+        return torch.from_numpy(a).to(device)
+    return to_dev(a, cache_code, device)
+
+
+def call(device, c, code, cache_code, noalloc, max_ctx):
+    """One decode through the C ABI; returns the output words on the host."""
+    lib = _lib.load()
+    dt = {orc.F32: _lib.DTYPE_F32, orc.BF16: _lib.DTYPE_BF16, orc.F16: _lib.DTYPE_F16}[code]
+    cdt = _lib.DTYPE_FP8_E4M3 if cache_code == orc.FP8 else dt
+    q = to_dev(c["q"], code, device)
+    kc, vc = dev_cache(c["kc"], cache_code, device), dev_cache(c["vc"], cache_code, device)
+    bt, lens = u32(c["bt"], device), u32(c["lens"], device)
+    out = torch.full_like(q, float("nan"))
+    one = torch.ones(1, dtype=torch.float32, device=device)
+    ks = one.data_ptr() if cache_code == orc.FP8 else None
+    b = len(c["lens"])
+    stride_b, stride_h = kc.stride(0), kc.stride(1)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    common = (out.data_ptr(), q.data_ptr(), ks, ks, kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
+              bt.shape[1], lens.data_ptr(), None, max_ctx, D ** -0.5, 1.0, None, b, H, KVH, D, BS,
+              c["nb"], stride_b, stride_h, dt, cdt)
+    torch.cuda.synchronize()
+    if noalloc:
+        rc = lib.vpa_paged_attention_noalloc(*common, stream)
+    else:
+        n = lib.vpa_paged_attention_workspace_size(b, H, D, max_ctx)
+        ws = torch.empty(n, dtype=torch.uint8, device=device)
+        rc = lib.vpa_paged_attention(*common, ws.data_ptr(), n, stream)
+    assert rc == 0, lib.vpa_last_error().decode()
+    torch.cuda.synchronize()
+    return to_host(out)
+
+
+@pytest.mark.parametrize("code,cache_code", [(orc.BF16, orc.BF16), (orc.BF16, orc.FP8),
+                                             (orc.F32, orc.F32)])
+def test_noalloc_equals_workspace_entry_point_twice(device, code, cache_code):
+    rng = np.random.default_rng(31 + code + 7 * cache_code)
+    first = [int(x) for x in rng.integers(1, 4500, size=40)]
+    first[:4] = [4096, 2049, 2048, 1]  # multi-chunk and single-chunk rows
+    second = [int(x) for x in rng.integers(1, 1500, size=17)]
+    for lens in (first, second):
+        c = case(rng, code, lens, cache_code)
+        max_ctx = int(max(lens))
+        got = call(device, c, code, cache_code, True, max_ctx)
+        want = call(device, c, code, cache_code, False, max_ctx)
+        assert np.array_equal(got, want), f"batch {len(lens)}: noalloc differs from workspace call"
+        assert np.all(np.isfinite(orc.to_f32(got, code)))
+    # the second (smaller) call against the oracle
+    ref = orc.paged_attention(c["q"], c["kc"], c["vc"], c["bt"], c["lens"], max_ctx, D ** -0.5,
+                              dtype=code, kv_dtype=orc.FP8 if cache_code == orc.FP8 else None)
+    assert_attention_close(orc.to_f32(got, code), ref, code, "noalloc second call")
+
+
+def test_noalloc_rejects_a_call_beyond_its_scratch(device):
+    """4096 sequences of up to 16384 tokens need 335 MB of partial rows: a
+    clear VPA_ERR_WORKSPACE, nothing launched."""
+    lib = _lib.load()
+    fake = 1 << 20
+    rc = lib.vpa_paged_attention_noalloc(fake, fake, None, None, fake, fake, fake, 1024, fake,
+                                         None, 16384, 0.088, 1.0, None, 4096, H, KVH, D, BS, 100,
+                                         KVH * D * BS, D * BS, _lib.DTYPE_BF16, _lib.DTYPE_BF16,
+                                         None)
+    assert rc == _lib.VPA_ERR_WORKSPACE
+    assert "static scratch" in lib.vpa_last_error().decode()
