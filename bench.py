@@ -339,7 +339,7 @@ def device_step(w, dev, reps, warmup):
         st.end(logits)
 
     def full():
-        st.tokens.consume()
+        st.tokens.consume(st.allocator.slot_mapping)
         st.allocator.step(st.tokens.finished)
         work()
 

@@ -242,6 +242,10 @@ int vpa_paged_attention_noalloc(void* out, const void* query, const float* k_sca
  * out_dtype f32 / f16 / bf16: each value is (float)byte * scale rounded to
  * nearest even, with k_scale / v_scale device pointers to one f32 each.
  * num_seqs and block_table_stride are at most 65535 (VPA_ERR_UNSUPPORTED).
+ * Each sequence's kv_len (cu_seqlens_kv[s+1] - cu_seqlens_kv[s]) must not
+ * exceed block_table_stride * block_size: the lengths live on the device, so
+ * this cannot be checked before the launch, and rows past the table width
+ * are left unwritten.
  */
 int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
                         const void* value_cache, const float* k_scale, const float* v_scale,
@@ -321,10 +325,19 @@ int vpa_argmax_rows(const void* logits, int64_t row_stride, int32_t vocab, int32
  * compacted out of the batch, so a captured decode graph keeps its shape.
  * input_ids[r] receives the row's input id; *active_count the number of rows
  * that fed a real token (the 4 bytes a host loop reads when it checks for
- * completion). finished is u8 per row. All pointers are device memory; no
- * host synchronisation; safe under stream capture.
+ * completion). finished is u8 per row.
+ * prev_slot_mapping (i64 [num_rows], may be NULL) is the previous step's
+ * slot_mapping: a row that is not finished and whose previous slot is
+ * negative did not run in that step (no block for its token, as
+ * try_allocate_slots failing keeps a slot out of the forward,
+ * paged_batch_engine.rs:209-227), so it feeds the same input id again,
+ * appends nothing and ignores its pending id (the argmax of a forward it
+ * took no part in); it counts as active. NULL: every unfinished row
+ * consumes its pending id. All pointers are device memory; no host
+ * synchronisation; safe under stream capture.
  */
-int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished, uint32_t* generated,
+int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished,
+                              const int64_t* prev_slot_mapping, uint32_t* generated,
                               uint32_t* gen_len, int32_t gen_capacity, const uint32_t* eos_ids,
                               int32_t num_eos, uint32_t eos_fill_id, uint32_t* input_ids,
                               uint32_t* active_count, int32_t num_rows, void* stream);
@@ -338,7 +351,7 @@ int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished, uint3
  *   free_ring    [free_ring_capacity] u32, free_ring_state [2] u32 = {head,
  *                count}: the free block ids in hand-out order (a FIFO ring;
  *                capacity >= the pool's block count)
- * It restates PagedBlockManager (vasr-models/src/model/paged_cache_runtime.rs:
+ * It restates PagedBlockManager (vasr-paged-attn/src/paged_cache_runtime.rs:
  * 217-380: a FIFO free list, initially ids 1..num_blocks-1, handed out from
  * the front, released blocks pushed to the back last block first, block 0
  * never) and decode_metadata_for_batch_step (vasr-paged-attn/src/

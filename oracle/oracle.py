@@ -80,7 +80,7 @@ def lib():
         L.oracle_prefill_attention_kv_f64.restype = None
         L.oracle_argmax_rows.argtypes = [_i32, _p, _i64, _i32, _i32, _p]
         L.oracle_argmax_rows.restype = None
-        L.oracle_decode_consume_tokens.argtypes = [_p, _p, _p, _p, _i32, _p, _i32,
+        L.oracle_decode_consume_tokens.argtypes = [_p, _p, _p, _p, _p, _i32, _p, _i32,
                                                    ctypes.c_uint32, _p, _p, _i32]
         L.oracle_decode_consume_tokens.restype = None
         L.oracle_prefill_attention_f64.argtypes = [_i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i32,
@@ -292,14 +292,21 @@ def argmax_rows(logits: np.ndarray, dtype=None) -> np.ndarray:
     return out
 
 
-def decode_consume_tokens(next_ids, finished, generated, gen_len, eos_ids, eos_fill_id):
-    """In-place step-start bookkeeping; returns (input_ids, active_count)."""
+def decode_consume_tokens(next_ids, finished, generated, gen_len, eos_ids, eos_fill_id,
+                          prev_slots=None, input_ids=None):
+    """In-place step-start bookkeeping; returns (input_ids, active_count).
+    ``prev_slots``: the previous step's slot_mapping (rows with a negative
+    slot did not run and feed ``input_ids`` again); ``input_ids``: the
+    previous step's input ids (read for those rows)."""
     b, cap = generated.shape
     eos = np.ascontiguousarray(eos_ids, dtype=np.uint32)
-    inp = np.zeros(b, dtype=np.uint32)
+    inp = (np.zeros(b, dtype=np.uint32) if input_ids is None
+           else np.array(input_ids, dtype=np.uint32, copy=True))
     cnt = np.zeros(1, dtype=np.uint32)
+    prev = None if prev_slots is None else np.ascontiguousarray(prev_slots, dtype=np.int64)
     lib().oracle_decode_consume_tokens(_ptr(np.ascontiguousarray(next_ids, dtype=np.uint32)),
-                                       _ptr(finished), _ptr(generated), _ptr(gen_len), cap,
+                                       _ptr(finished), None if prev is None else _ptr(prev),
+                                       _ptr(generated), _ptr(gen_len), cap,
                                        _ptr(eos), eos.size, int(eos_fill_id), _ptr(inp),
                                        _ptr(cnt), b)
     return inp, int(cnt[0])

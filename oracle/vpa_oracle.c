@@ -555,16 +555,24 @@ void oracle_argmax_rows(int dtype, const void* logits, int64_t row_stride, int v
  * any other id is appended to its generated list (up to gen_capacity) and
  * becomes its input id. Finished rows get eos_fill_id as input (the
  * reference's pad id, eos_token_ids[0], paged_batch_engine.rs:193-195).
- * *active_count = rows that fed a real token.
+ * *active_count = rows that fed a real token. With prev_slots (the
+ * previous step's slot_mapping), an unfinished row whose previous slot is
+ * negative did not run: it feeds input_ids[r] again and consumes nothing
+ * (the reference keeps a slot that could not allocate out of the forward
+ * with its pending id, paged_batch_engine.rs:209-227).
  */
 void oracle_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished,
-                                  uint32_t* generated, uint32_t* gen_len, int gen_capacity,
+                                  const int64_t* prev_slots, uint32_t* generated,
+                                  uint32_t* gen_len, int gen_capacity,
                                   const uint32_t* eos_ids, int num_eos, uint32_t eos_fill_id,
                                   uint32_t* input_ids, uint32_t* active_count, int num_rows) {
   uint32_t active = 0;
   for (int r = 0; r < num_rows; ++r) {
     uint32_t feed = eos_fill_id;
-    if (!finished[r]) {
+    if (!finished[r] && prev_slots != NULL && prev_slots[r] < 0) {
+      feed = input_ids[r];
+      ++active;
+    } else if (!finished[r]) {
       const uint32_t tok = next_ids[r];
       int eos = 0;
       for (int e = 0; e < num_eos; ++e) eos |= tok == eos_ids[e];

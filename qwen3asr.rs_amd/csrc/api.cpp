@@ -512,7 +512,7 @@ int vpa_chunked_prefill_paged_attention(
     return fail(VPA_ERR_UNSUPPORTED,
                 "%s: no MFMA kernel for dtype=%s cache=%s head_dim=%d block_size=%d group=%d "
                 "(bf16/f16, head_dim 64/128, block_size 8/16/32, 1/2/4 query heads per kv "
-                "head; fp8 caches: head_dim 128, block_size 16/32)",
+                "head; fp8 caches: head_dim 64/128, block_size 16/32)",
                 op, dtype_name(dtype), dtype_name(cache_dtype), head_dim, block_size, group);
   if (num_seqs == 0 || max_query_len == 0 || total_query_rows == 0) return VPA_OK;
   {
@@ -567,7 +567,8 @@ int vpa_argmax_rows(const void* logits, int64_t row_stride, int32_t vocab, int32
                                            static_cast<hipStream_t>(stream)));
 }
 
-int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished, uint32_t* generated,
+int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished,
+                              const int64_t* prev_slot_mapping, uint32_t* generated,
                               uint32_t* gen_len, int32_t gen_capacity, const uint32_t* eos_ids,
                               int32_t num_eos, uint32_t eos_fill_id, uint32_t* input_ids,
                               uint32_t* active_count, int32_t num_rows, void* stream) {
@@ -584,8 +585,8 @@ int vpa_decode_consume_tokens(const uint32_t* next_ids, uint8_t* finished, uint3
   if (num_rows > 0 && (next_ids == nullptr || finished == nullptr || gen_len == nullptr ||
                        input_ids == nullptr || (gen_capacity > 0 && generated == nullptr)))
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: state buffers must be non-null", op);
-  return hip_status(op, launch_consume_tokens(next_ids, finished, generated, gen_len,
-                                              gen_capacity, eos_ids, num_eos, eos_fill_id,
+  return hip_status(op, launch_consume_tokens(next_ids, finished, prev_slot_mapping, generated,
+                                              gen_len, gen_capacity, eos_ids, num_eos, eos_fill_id,
                                               input_ids, active_count, num_rows,
                                               static_cast<hipStream_t>(stream)));
 }

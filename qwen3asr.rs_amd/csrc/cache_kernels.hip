@@ -165,7 +165,11 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
 
   // General path: arbitrary slot per token. Lanes run along the token axis so
   // that tokens sharing a block still produce adjacent addresses.
-  bool all_alone = true;  // no two tokens of the workgroup share a block
+  // No two neighbouring tokens of the workgroup share a block (decode: one
+  // token per sequence). Only neighbours are compared: tokens that share a
+  // block without being adjacent (slots 5, 100, 6) also take the streaming
+  // stores, which stay correct, only slower for that rare pattern.
+  bool all_alone = true;
 #pragma unroll
   for (int i = 1; i < BS; ++i)
     all_alone = all_alone && !(slots[i] >= 0 && slots[i - 1] >= 0 &&

@@ -3,7 +3,7 @@
 // The reference builds every decode step's metadata on the host and copies
 // it over: the block manager grows each running request by a block when its
 // next token starts one (PagedBlockManager::allocate_slots /
-// try_allocate_slots, vasr-models/src/model/paged_cache_runtime.rs:217-380;
+// try_allocate_slots, vasr-paged-attn/src/paged_cache_runtime.rs:217-380;
 // FIFO free list handed out from the front, released blocks pushed to the
 // back last block first), then decode_metadata_for_batch_step
 // (vasr-paged-attn/src/paged_kv_cache.rs:924-1059) turns block tables and

@@ -712,8 +712,9 @@ hipError_t dispatch_group(int group, const PrefillArgs& a, const CacheGeom& g,
   }
 }
 
-// fp8 caches: head_dim 128, block_size 16 or 32 (a 32-key tile is then 256
-// 16-byte units, one DMA per lane of the workgroup)
+// fp8 caches: head_dim 64 or 128, block_size 16 or 32 (at head_dim 128 a
+// 32-key tile is 256 16-byte units, one DMA per lane of the workgroup; at 64,
+// 128 units moved by two of the four waves)
 template <typename T, typename C>
 hipError_t dispatch_shape(int group, const PrefillArgs& a, const CacheGeom& g,
                           hipStream_t stream) {

@@ -103,7 +103,7 @@ constexpr int kConsumeThreads = 1024;
 
 __global__ __launch_bounds__(kConsumeThreads) void consume_tokens_kernel(
     const uint32_t* __restrict__ next_ids, uint8_t* __restrict__ finished,
-    uint32_t* __restrict__ generated, uint32_t* __restrict__ gen_len, int32_t gen_capacity,
+    const int64_t* __restrict__ prev_slots, uint32_t* __restrict__ generated, uint32_t* __restrict__ gen_len, int32_t gen_capacity,
     const uint32_t* __restrict__ eos_ids, int32_t num_eos, uint32_t eos_fill_id,
     uint32_t* __restrict__ input_ids, uint32_t* __restrict__ active_count, int32_t num_rows) {
   __shared__ uint32_t s_cnt[kConsumeThreads / 64];
@@ -111,7 +111,12 @@ __global__ __launch_bounds__(kConsumeThreads) void consume_tokens_kernel(
   uint32_t active = 0;
   for (int r = tid; r < num_rows; r += kConsumeThreads) {
     uint32_t feed = eos_fill_id;
-    if (!finished[r]) {
+    if (!finished[r] && prev_slots != nullptr && prev_slots[r] < 0) {
+      // the previous step did not run this row (no block for its token): it
+      // feeds the same input again and its pending id is stale
+      feed = input_ids[r];
+      ++active;
+    } else if (!finished[r]) {
       const uint32_t tok = next_ids[r];
       bool eos = false;
       for (int e = 0; e < num_eos; ++e) eos = eos || tok == eos_ids[e];
@@ -165,12 +170,12 @@ hipError_t launch_argmax_rows(int dtype, const void* logits, int64_t row_stride,
 }
 
 hipError_t launch_consume_tokens(const uint32_t* next_ids, uint8_t* finished,
-                                 uint32_t* generated, uint32_t* gen_len, int32_t gen_capacity,
+                                 const int64_t* prev_slot_mapping, uint32_t* generated, uint32_t* gen_len, int32_t gen_capacity,
                                  const uint32_t* eos_ids, int32_t num_eos, uint32_t eos_fill_id,
                                  uint32_t* input_ids, uint32_t* active_count, int32_t num_rows,
                                  hipStream_t stream) {
   hipLaunchKernelGGL(consume_tokens_kernel, dim3(1), dim3(kConsumeThreads), 0, stream, next_ids,
-                     finished, generated, gen_len, gen_capacity, eos_ids, num_eos, eos_fill_id,
+                     finished, prev_slot_mapping, generated, gen_len, gen_capacity, eos_ids, num_eos, eos_fill_id,
                      input_ids, active_count, num_rows);
   return hipGetLastError();
 }

@@ -142,7 +142,7 @@ hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t m
 hipError_t launch_argmax_rows(int dtype, const void* logits, int64_t row_stride, int32_t vocab,
                               int32_t num_rows, uint32_t* out, hipStream_t stream);
 hipError_t launch_consume_tokens(const uint32_t* next_ids, uint8_t* finished,
-                                 uint32_t* generated, uint32_t* gen_len, int32_t gen_capacity,
+                                 const int64_t* prev_slot_mapping, uint32_t* generated, uint32_t* gen_len, int32_t gen_capacity,
                                  const uint32_t* eos_ids, int32_t num_eos, uint32_t eos_fill_id,
                                  uint32_t* input_ids, uint32_t* active_count, int32_t num_rows,
                                  hipStream_t stream);

@@ -62,7 +62,7 @@ SIGNATURES = {
         _i32, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
     "vpa_argmax_rows": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p]),
     "vpa_decode_consume_tokens": (ctypes.c_int, [
-        _p, _p, _p, _p, _i32, _p, _i32, _u32, _p, _p, _i32, _p]),
+        _p, _p, _p, _p, _p, _i32, _p, _i32, _u32, _p, _p, _i32, _p]),
     "vpa_allocate_rows": (ctypes.c_int, [_p, _i32, _p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "vpa_decode_step_metadata": (ctypes.c_int, [
         _p, _i32, _p, _p, _p, _p, _p, _i32, _i32, _p, _p, _p, _i32, _p]),

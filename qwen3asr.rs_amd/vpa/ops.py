@@ -354,12 +354,18 @@ class DecodeTokenState:
         """next_ids <- argmax of the step's logits rows (all rows of the batch)."""
         argmax_token_ids_from_logits(logits, out=self.next_ids)
 
-    def consume(self) -> None:
+    def consume(self, prev_slot_mapping: Optional[torch.Tensor] = None) -> None:
         """Step start (paged_batch_engine.rs:640-667): pending EOS ids finish
         their rows, other pending ids are appended and become input_ids;
-        finished rows feed the EOS fill id."""
+        finished rows feed the EOS fill id. With the previous step's
+        ``prev_slot_mapping`` (i64 [batch]), a row that did not run in that
+        step (negative slot) feeds its input id again and appends nothing."""
+        if prev_slot_mapping is not None and (prev_slot_mapping.dtype != torch.int64 or
+                                              prev_slot_mapping.shape != (self.batch,)):
+            raise _err(f"prev_slot_mapping must be i64 [{self.batch}]")
         check(_lib.load().vpa_decode_consume_tokens(
-            self.next_ids.data_ptr(), self.finished.data_ptr(), self.generated.data_ptr(),
+            self.next_ids.data_ptr(), self.finished.data_ptr(), _ptr(prev_slot_mapping),
+            self.generated.data_ptr(),
             self.gen_len.data_ptr(), self.capacity, self.eos_ids.data_ptr(),
             self.eos_ids.numel(), self.eos_fill_id, self.input_ids.data_ptr(),
             self.active_count.data_ptr(), self.batch, _stream(self.next_ids)))

@@ -25,7 +25,11 @@ Every layer shares the allocator's block tables (one block manager for the
 model, each layer its own cache tensors), as the reference does. Rows that
 finished feed the EOS fill id and get the PAD slot; a row the pool cannot
 grow stalls for the step (its slot is PAD and its position does not move;
-``allocator.status[0]`` counts them)."""
+``allocator.status[0]`` counts them): the next step's bookkeeping sees the
+PAD slot left in ``allocator.slot_mapping``, feeds the row's input id again
+and appends nothing (the argmax of a forward the row took no part in is
+dropped), as the reference keeps a slot that could not allocate out of the
+forward with its pending id (paged_batch_engine.rs:209-227)."""
 
 from __future__ import annotations
 
@@ -57,6 +61,10 @@ class DeviceDecodeStep:
         ok = self.allocator.allocate(prompt_lens)
         self.allocator.positions.copy_(prompt_lens.to(torch.uint32))
         self.tokens.finished.copy_((ok == 0).to(torch.uint8))
+        # no step has run yet: every admitted row consumes its pending id at
+        # the first step (a non-negative previous slot; block 0 is the null
+        # block, nothing is written there before the first step's metadata)
+        self.allocator.slot_mapping.zero_()
         return ok
 
     def begin(self, key_cache: torch.Tensor, value_cache: torch.Tensor,
@@ -64,7 +72,7 @@ class DeviceDecodeStep:
         """Step start: pending ids consumed (EOS rows finish), blocks grown,
         this step's slot_mapping / context_lens and the decode work list
         built (the caches of any layer give the geometry and cache type)."""
-        self.tokens.consume()
+        self.tokens.consume(self.allocator.slot_mapping)
         self.allocator.step(self.tokens.finished)
         ops.paged_attention_plan(self.allocator.context_lens, self.max_context_len, self.cols,
                                  self.num_heads, key_cache, value_cache, query_dtype,

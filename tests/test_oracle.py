@@ -513,6 +513,63 @@ def _reference_decode_loop(pending, steps_logits_ids, eos_ids):
     return finished, generated
 
 
+def _reference_decode_loop_with_stalls(pending, steps_new_ids, stalls, eos_ids):
+    """paged_batch_engine.rs:209-300 with allocation failures: a slot whose
+    try_allocate_slots fails at a step is not decodable, stays out of the
+    forward and keeps its pending id; decodable slots consume their pending
+    id (an EOS id finishes the slot), feed it and take the forward's argmax."""
+    batch = len(pending)
+    next_ids = list(pending)
+    finished = [False] * batch
+    generated = [[] for _ in range(batch)]
+    for n, new_ids in enumerate(steps_new_ids):
+        for i in range(batch):
+            if finished[i] or i in stalls[n]:
+                continue
+            tok = next_ids[i]
+            if tok in eos_ids:
+                finished[i] = True
+                continue
+            generated[i].append(tok)
+            next_ids[i] = int(new_ids[i])
+    return finished, generated
+
+
+def test_consume_oracle_with_stalls_equals_reference_loop():
+    """Rows whose block allocation fails: the device loop consumes before it
+    allocates, so a row that then stalls has appended its token already; the
+    next step's consume sees the row's PAD slot, feeds the same input again
+    and drops the pending id of the forward the row took no part in. The
+    generated lists and finished flags end equal to the reference's, where a
+    slot that cannot allocate is skipped with its pending id kept."""
+    rng = np.random.default_rng(17)
+    batch, steps, cap = 29, 16, 24
+    eos = [2, 5]
+    pending = rng.integers(0, 9, size=batch)
+    new_ids = [rng.integers(0, 9, size=batch) for _ in range(steps)]
+    stalls = [set(rng.choice(batch, size=int(rng.integers(0, 8)), replace=False).tolist())
+              for _ in range(steps - 1)] + [set()]  # the last step serves every row
+    want_fin, want_gen = _reference_decode_loop_with_stalls(list(pending), new_ids, stalls, eos)
+    nid = pending.astype(np.uint32)
+    fin = np.zeros(batch, np.uint8)
+    gen = np.zeros((batch, cap), np.uint32)
+    glen = np.zeros(batch, np.uint32)
+    inp = np.zeros(batch, np.uint32)
+    prev = np.zeros(batch, np.int64)  # admission: every row counts as having run
+    stalled_rows_seen = 0
+    for n in range(steps):
+        inp, active = orc.decode_consume_tokens(nid, fin, gen, glen, eos, eos[0], prev, inp)
+        assert active == int((fin == 0).sum())
+        ran = np.array([not fin[i] and i not in stalls[n] for i in range(batch)])
+        stalled_rows_seen += int((~ran & (fin == 0)).sum())
+        prev = np.where(ran, 0, -1).astype(np.int64)
+        # forward + argmax over every row; stalled rows get a junk id
+        nid = np.where(ran, new_ids[n], 1 << 30).astype(np.uint32)
+    assert stalled_rows_seen > 0
+    assert fin.astype(bool).tolist() == want_fin
+    assert [gen[i, :glen[i]].tolist() for i in range(batch)] == want_gen
+
+
 def test_consume_oracle_equals_reference_loop_with_compaction():
     """Feeding finished rows the fill id instead of compacting them gives the
     reference's generated lists and finished flags after every step."""
