@@ -17,12 +17,16 @@ replays its decode step from a CUDA graph, vasr-paged-attn/src/cuda_graph.rs:
 two ends of each timed region.
 
 Prints one JSON line. `value` is the whole-step HBM throughput: algorithmic
-bytes of all appends and decodes of a step divided by the step time. The
-`roofline` object covers the dominant op (paged_attention: plan, rows and
-merge launches) timed back to back over the step's layers; `append_gbps`
-likewise for reshape_and_cache; `cpu_baseline` times the oracle's
-restatement of the reference CPU path on a bounded sample; `prefill_c4`
-reports the chunked-prefill row (append + MFMA prefill) on c4.
+bytes of all appends and decodes of a step divided by the step time. Each op
+is also timed on its own from a graph of the step's layers: the `roofline`
+object covers the dominant op (paged_attention: plan, rows and merge
+launches), with the rate of the same reads with no compute
+(`vpa_paged_cache_read`) as `measured_peak`; `decode_in_step_*` is the
+decode as the step runs it, right after its layer's append (step minus the
+appends alone); `append_*` is reshape_and_cache; `decode_seeds` repeats the
+decode over c3 seeds 1-5; `cpu_baseline` times the oracle's restatement of
+the reference CPU path on a bounded sample; `prefill_c4` reports the
+chunked-prefill row (append + MFMA prefill) on c4.
 """
 
 from __future__ import annotations
@@ -61,6 +65,8 @@ def parse():
                     help="skip the fp8-cache decode measurement")
     ap.add_argument("--no-device-step", dest="device_step", action="store_false",
                     help="skip the device-resident whole-step measurement")
+    ap.add_argument("--seeds", default="1,2,3,4,5",
+                    help="c3 seeds of the decode sweep (empty: skip it)")
     return ap.parse_args()
 
 
@@ -226,6 +232,7 @@ def cpu_baseline(w, layers, budget_s):
         "value": round(gbps, 3),
         "unit": "GB/s",
         "cores": int(threads),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"{groups} group(s) of up to {group} sequences of one layer of {w.name} "
                    f"({seq_layers} sequence-layers of {w.num_seqs} x {len(layers)}, append + "
@@ -513,6 +520,127 @@ def prefill_c4(dev, reps=10):
     }
 
 
+def graph_of(fn):
+    """fn's launches captured once as a HIP graph (after a device sync)."""
+    import torch
+
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def read_ops(layers, ctx, w, ws, sink):
+    """Per layer: the decode's reads with no compute (vpa_paged_cache_read),
+    over the step's work list: the achievable gather rate of the pattern."""
+    import vpa
+
+    plan_step(layers, ctx, w, ws)
+    for L in layers:
+        vpa.paged_cache_read(L["kc"], L["vc"], L["bt"], w.max_context_len, w.num_heads, ws, sink)
+
+
+def op_timings(layers, ctx, w, ws, reps, warmup, sink=None):
+    """us per layer of the step's ops, each from a graph of all the step's
+    layers replayed back to back (launch gaps of the eager path do not enter):
+    decode alone (plan + 28 planned calls), append alone, the whole step, the
+    decode inside the step (step minus the appends alone: the decode that
+    follows its layer's append, thinker_text.rs:1101-1139, with whatever the
+    append leaves behind charged to it) and, with `sink`, the read ceiling."""
+    nl = len(layers)
+    graphs = {
+        "decode": graph_of(lambda: decode_ops(layers, ctx, w, ws)),
+        "append": graph_of(lambda: append_ops(layers)),
+        "step": graph_of(lambda: run_step(layers, ctx, w, ws)),
+    }
+    if sink is not None:
+        graphs["read"] = graph_of(lambda: read_ops(layers, ctx, w, ws, sink))
+    res = {}
+    for name, g in graphs.items():
+        for _ in range(warmup):
+            g.replay()
+        res[name] = timed_ms(g.replay, reps) * 1e3 / nl  # us per layer
+    res["decode_in_step"] = res["step"] - res["append"]
+    return res
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def traffic_from_profile(w):
+    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary
+    of this workload, with the hash of the decode kernels' source it was
+    measured on: null when that source has changed since (stale)."""
+    import hashlib
+
+    path = os.path.join("profiles", f"paged_decode_{w.name}_traffic.json")
+    full = os.path.join(ROOT, path)
+    src = os.path.join(ROOT, "qwen3asr.rs_amd", "csrc", "decode_kernels.hip")
+    if not os.path.exists(full):
+        return None, {"source": path, "status": "absent"}
+    with open(full) as f:
+        j = json.load(f)
+    with open(src, "rb") as f:
+        sha = hashlib.sha256(f.read()).hexdigest()[:16]
+    measured = j.get("decode_kernels_sha256_16")
+    stale = measured != sha
+    info = {"source": path, "measured_on_decode_kernels_sha256_16": measured,
+            "current_decode_kernels_sha256_16": sha, "status": "stale" if stale else "current",
+            "how": "rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of bench.py, per-dispatch "
+                   "KiB scaled by a plain-copy calibration (commands in the file)"}
+    return (None if stale else j.get("bytes_per_launch")), info
+
+
+def decode_seeds(dev, seeds, reps, warmup):
+    """The c3 decode over several seeds of its generation rule (each seed
+    draws its own lengths and tables): decode alone and inside the step, us
+    per layer and fraction of the HBM peak, with each seed's mean context."""
+    import numpy as np
+    import torch
+
+    import vpa
+    from vpa import workloads
+
+    rows = []
+    for sd in seeds:
+        w = workloads.c3(seed=sd)
+        layers, ctx = device_tensors(w, dev)
+        ws = vpa.paged_attention_workspace(w.num_seqs, w.num_heads, w.head_dim,
+                                           w.max_context_len, dev)
+        run_step(layers, ctx, w, ws)
+        t = op_timings(layers, ctx, w, ws, reps, warmup)
+        b = w.decode_bytes_per_layer()
+        rows.append({
+            "seed": sd,
+            "mean_context": round(float(np.mean(w.context_lens)), 1),
+            "decode_us": round(t["decode"], 2),
+            "decode_frac_of_peak": round(b / (t["decode"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+            "decode_in_step_us": round(t["decode_in_step"], 2),
+            "decode_in_step_frac_of_peak": round(
+                b / (t["decode_in_step"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        })
+        del layers, ws, ctx
+        torch.cuda.empty_cache()
+    return {
+        "workload": "c3",
+        "seeds": rows,
+        "min_decode_frac_of_peak": min(r["decode_frac_of_peak"] for r in rows),
+        "min_decode_in_step_frac_of_peak": min(r["decode_in_step_frac_of_peak"] for r in rows),
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -530,6 +658,7 @@ def main():
     layers, ctx = device_tensors(w, dev)
     ws = vpa.paged_attention_workspace(w.num_seqs, w.num_heads, w.head_dim, w.max_context_len,
                                        dev)
+    sink = torch.zeros(1, dtype=torch.uint32, device=dev)
     nl = len(layers)
 
     for _ in range(args.warmup):
@@ -542,10 +671,7 @@ def main():
     step = lambda: run_step(layers, ctx, w, ws)  # noqa: E731
     execution = "eager launches"
     if not args.eager:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            run_step(layers, ctx, w, ws)
-        torch.cuda.synchronize()
+        graph = graph_of(step)
         step = graph.replay
         execution = "hip graph replay of the whole step"
         for _ in range(args.warmup):
@@ -554,32 +680,34 @@ def main():
     ms_per_step = timed_ms(step, args.steps)
     wall = time.perf_counter() - wall0
 
-    # the two ops on their own, back to back over the same layers (the
-    # per-op figures and the roofline), and the eager step for comparison
+    # the eager step for comparison, then each op on its own (graphs of the
+    # step's layers): decode, append, decode inside the step, read ceiling
     eager_ms = timed_ms(lambda: run_step(layers, ctx, w, ws), args.steps)
-    decode_ms = timed_ms(lambda: decode_ops(layers, ctx, w, ws), args.steps)
-    append_ms = timed_ms(lambda: append_ops(layers), args.steps)
+    ops = op_timings(layers, ctx, w, ws, args.steps, args.warmup, sink=sink)
 
     dec_bytes = w.decode_bytes_per_layer()
     app_bytes = w.append_bytes_per_layer()
     step_bytes = nl * (dec_bytes + app_bytes)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    dec_launch_ms = decode_ms / nl
-    app_launch_ms = append_ms / nl
-    dec_gbps = dec_bytes / (dec_launch_ms * 1e-3) / 1e9
-    app_gbps = app_bytes / (app_launch_ms * 1e-3) / 1e9
 
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"paged_decode_{w.name}_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+    def gbps(nbytes, us):
+        return nbytes / (us * 1e-6) / 1e9
+
+    dec_gbps = gbps(dec_bytes, ops["decode"])
+    in_step_gbps = gbps(dec_bytes, ops["decode_in_step"])
+    app_gbps = gbps(app_bytes, ops["append"])
+    read_gbps = gbps(dec_bytes, ops["read"])
+    traffic, traffic_info = traffic_from_profile(w)
 
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(w, layers, args.cpu_seconds)
     del layers, ws
     torch.cuda.empty_cache()
+    seeds = None
+    if args.seeds and w.name == "c3":
+        seeds = decode_seeds(dev, [int(x) for x in args.seeds.split(",")], args.steps,
+                             args.warmup)
     f8 = None
     if args.fp8 and w.dtype == "bf16":
         f8 = decode_fp8(w, dev, args.steps)
@@ -613,6 +741,7 @@ def main():
             "head_dim": w.head_dim,
             "block_size": w.block_size,
             "context_tokens": int(w.context_lens.sum()),
+            "mean_context": round(float(w.context_lens.mean()), 1),
             "max_context_len": w.max_context_len,
             "seed": w.seed,
         },
@@ -620,22 +749,32 @@ def main():
         "eager_value": round(step_bytes / (eager_ms * 1e-3) / 1e9, 2),
         "decode_gbps": round(dec_gbps, 2),
         "decode_frac_of_peak": round(dec_gbps / HBM_PEAK_GBPS, 4),
+        "decode_in_step_us": round(ops["decode_in_step"], 2),
+        "decode_in_step_gbps": round(in_step_gbps, 2),
+        "decode_in_step_frac_of_peak": round(in_step_gbps / HBM_PEAK_GBPS, 4),
         "append_gbps": round(app_gbps, 2),
-        "append_us_per_launch": round(app_launch_ms * 1e3, 2),
+        "append_us_per_launch": round(ops["append"], 2),
         "wall_s_timed_region": round(wall, 4),
         "roofline": {
             "kernel": "paged_attention (rows + merge launches per layer, plus one plan "
-                      "launch per step), back to back over the step's layers",
+                      "launch per step), a graph of the step's decodes replayed back to back",
             "bound": "hbm",
             "achieved": round(dec_gbps, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_info,
             "algorithmic_bytes_per_launch": dec_bytes,
-            "us_per_launch": round(dec_launch_ms * 1e3, 2),
+            "us_per_launch": round(ops["decode"], 2),
+            "measured_peak": round(read_gbps, 2),
+            "measured_peak_what": "vpa_paged_cache_read: the decode's tile reads (same work "
+                                  "list, waves and 16-byte loads) with no compute, same layers",
+            "frac_of_measured": round(dec_gbps / read_gbps, 4),
+            "read_us_per_launch": round(ops["read"], 2),
         },
         "cpu_baseline": cpu,
+        "decode_seeds": seeds,
         "decode_fp8": f8,
         "device_step": dstep,
         "prefill_c4": pf,

@@ -228,6 +228,27 @@ int vpa_paged_attention_noalloc(void* out, const void* query, const float* k_sca
                                 int32_t dtype, int32_t cache_dtype, void* stream);
 
 /*
+ * paged_cache_read — a measurement kernel with no counterpart in the
+ * reference: reads every K and V byte of each sequence's context through its
+ * block table exactly as the decode does (the work list that
+ * vpa_paged_attention_plan left in `workspace` for the same lengths and
+ * sizes, the same split of each chunk's blocks over the waves, the same
+ * 16-byte loads) and computes nothing but an XOR of the bytes. Its rate is
+ * the achievable gather bandwidth of the decode's access pattern on the
+ * device, the ceiling against which the decode's own rate is read. *sink
+ * (device u32) is written only where a lane's checksum equals `magic`.
+ * 16-bit or fp8 caches, head_dim <= 128, (block, head) tiles of 1, 2, 4 or
+ * 8 KiB.
+ */
+int vpa_paged_cache_read(const void* key_cache, const void* value_cache,
+                         const uint32_t* block_tables, int32_t block_table_stride,
+                         int32_t max_context_len, int32_t num_seqs, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                         int64_t num_blocks, int64_t cache_block_stride,
+                         int64_t cache_head_stride, int32_t cache_dtype, void* workspace,
+                         size_t workspace_bytes, uint32_t magic, uint32_t* sink, void* stream);
+
+/*
  * gather_kv_cache — copy each sequence's first kv_len tokens out of the paged
  * cache into packed rows.
  * Replaces mistralrs_paged_attn::gather_kv_cache(key_cache, value_cache,

@@ -435,6 +435,51 @@ int vpa_paged_attention_plan(const uint32_t* context_lens, int32_t max_context_l
                                            static_cast<hipStream_t>(stream)));
 }
 
+int vpa_paged_cache_read(const void* key_cache, const void* value_cache,
+                         const uint32_t* block_tables, int32_t block_table_stride,
+                         int32_t max_context_len, int32_t num_seqs, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                         int64_t num_blocks, int64_t cache_block_stride,
+                         int64_t cache_head_stride, int32_t cache_dtype, void* workspace,
+                         size_t workspace_bytes, uint32_t magic, uint32_t* sink, void* stream) {
+  clear_error();
+  const char* op = "paged_cache_read";
+  int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
+                       cache_block_stride, cache_head_stride, key_cache, value_cache);
+  if (rc != VPA_OK) return rc;
+  if (!paged_read_supported(cache_dtype, head_dim, block_size))
+    return fail(VPA_ERR_UNSUPPORTED,
+                "%s: 16-bit or fp8 caches with head_dim <= 128 and whole-KiB tiles only", op);
+  if (num_seqs < 0 || num_heads <= 0 || max_context_len < 0 || block_table_stride < 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: bad sizes", op);
+  if (num_seqs == 0) return VPA_OK;
+  if (num_seqs > 65535)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: num_seqs=%d exceeds 65535", op, num_seqs);
+  if (max_context_len > kDecodeMaxPartitions * kDecodeMinPartitionTokens)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: max_context_len=%d exceeds %d", op, max_context_len,
+                kDecodeMaxPartitions * kDecodeMinPartitionTokens);
+  if (block_tables == nullptr || sink == nullptr)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: block_tables and sink must be non-null", op);
+  if (max_context_len > 0 && (int64_t)block_table_stride * block_size < max_context_len)
+    return fail(VPA_ERR_INVALID_ARGUMENT,
+                "%s: block_table_stride=%d too small for max_context_len=%d (block_size=%d)", op,
+                block_table_stride, max_context_len, block_size);
+  // the work list that vpa_paged_attention_plan left in the workspace
+  const size_t need = decode_workspace_bytes(num_seqs, num_heads, head_dim, max_context_len);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(VPA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", op, need,
+                workspace == nullptr ? (size_t)0 : workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned", op);
+  CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
+              cache_head_stride};
+  const DecodeWorkspace ws =
+      carve_decode_workspace(workspace, num_seqs, num_heads, head_dim, max_context_len);
+  return hip_status(op, launch_paged_read(cache_dtype, key_cache, value_cache, block_tables,
+                                          block_table_stride, max_context_len, num_seqs, g, ws,
+                                          magic, sink, static_cast<hipStream_t>(stream)));
+}
+
 int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
                         const void* value_cache, const float* k_scale, const float* v_scale,
                         const uint32_t* block_tables, int32_t block_table_stride,

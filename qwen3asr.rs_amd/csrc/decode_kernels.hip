@@ -1068,7 +1068,124 @@ hipError_t dispatch_decode(int dtype, int D, int BS, int group, A... args) {
   return hipErrorInvalidValue;
 }
 
+// Read ceiling of the decode's access pattern: the rows kernel's work items
+// and split of a chunk's blocks over its waves, each wave reading every K
+// then every V tile of its blocks with the same 16-byte loads (KPL per lane
+// per tile, each instruction 1 KiB contiguous), stages of NV loads double
+// buffered, and nothing computed but an XOR of the bytes. The checksum is
+// stored only when it equals `magic`, so the loads cannot be dropped.
+template <int BS, int KPL>
+__global__ __launch_bounds__(64 * kRowsWaves) void paged_read_kernel(
+    const uint4* __restrict__ key_cache, const uint4* __restrict__ value_cache,
+    const uint32_t* __restrict__ block_tables, int32_t block_table_stride,
+    int32_t num_kv_heads, int64_t num_blocks, int64_t block_stride_v, int64_t head_stride_v,
+    const uint2* __restrict__ items, const uint32_t* __restrict__ queue, int32_t num_seqs,
+    int32_t max_ctx, int32_t cap_tokens, uint32_t magic, uint32_t* __restrict__ sink) {
+  constexpr int NW = kRowsWaves;
+  constexpr int PB = kRowsPT / BS;  // blocks per wave partition
+  constexpr int NV = 8;             // loads per lane per stage
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const uint32_t w = blockIdx.x;
+  const int j = (int)(w % (uint32_t)num_kv_heads);
+  const uint32_t want = w / (uint32_t)num_kv_heads;
+  const uint32_t nitems = queue[1];
+  const uint2 item = items[want];
+  asm volatile("" ::"s"(nitems), "s"(item.x), "s"(item.y));
+  if (want >= nitems) return;
+  const int s = (int)(item.x >> 16);
+  const int chunk = (int)(item.x & 0xffffu);
+  if (s >= num_seqs) return;
+  const int L = clamp_context(item.y, max_ctx, cap_tokens);
+  if (L <= 0) return;
+  const int nblk = (L + BS - 1) / BS;
+  const int nchunks = (nblk + PB * NW - 1) / (PB * NW);
+  if (chunk >= nchunks) return;
+  const int c_begin = chunk * PB * NW;
+  const int c_nb = min(PB * NW, nblk - c_begin);
+  const int b_begin = c_begin + (c_nb * wave) / NW;
+  const int nb = c_begin + (c_nb * (wave + 1)) / NW - b_begin;
+  if (nb <= 0) return;
+  const uint32_t my_bt =
+      lane < nb ? block_tables[(int64_t)s * block_table_stride + b_begin + lane] : 0u;
+  const int64_t head_off = (int64_t)j * head_stride_v + lane;
+  const int n = 2 * nb * KPL;  // loads per lane: K tiles, then V tiles
+  auto load = [&](int i0, uint4(&buf)[NV]) {
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int i = i0 + u;
+      if (i < n) {
+        const int tile = i / KPL;
+        const bool v = tile >= nb;
+        const int bi = v ? tile - nb : tile;
+        const uint32_t phys = (uint32_t)__builtin_amdgcn_readlane((int)my_bt, bi);
+        const int64_t pb = (int64_t)phys < num_blocks ? (int64_t)phys : 0;
+        buf[u] = (v ? value_cache : key_cache)[pb * block_stride_v + head_off + 64 * (i % KPL)];
+      }
+    }
+  };
+  uint32_t acc = 0;
+  auto fold = [&](int i0, const uint4(&buf)[NV]) {
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+      if (i0 + u < n) acc ^= buf[u].x ^ buf[u].y ^ buf[u].z ^ buf[u].w;
+  };
+  uint4 a[NV], b[NV];
+  load(0, a);
+  load(NV, b);
+  for (int i = 0; i < n; i += 2 * NV) {
+    fold(i, a);
+    load(i + 2 * NV, a);
+    fold(i + NV, b);
+    load(i + 3 * NV, b);
+  }
+  if (acc == magic) sink[0] = acc;
+}
+
+template <int BS, int KPL>
+hipError_t launch_read_t(const void* kc, const void* vc, const uint32_t* bt, int32_t bts,
+                         int32_t max_ctx, int32_t num_seqs, const CacheGeom& g, int elem_bytes,
+                         const DecodeWorkspace& ws, uint32_t magic, uint32_t* sink,
+                         hipStream_t stream) {
+  const int max_chunks = max(1, (max_ctx + kDecodeChunk - 1) / kDecodeChunk);
+  const int64_t units = (int64_t)num_seqs * max_chunks * g.num_kv_heads;
+  const int64_t per_vec = 16 / elem_bytes;
+  hipLaunchKernelGGL((paged_read_kernel<BS, KPL>), dim3((unsigned)units), dim3(64 * kRowsWaves),
+                     0, stream, static_cast<const uint4*>(kc), static_cast<const uint4*>(vc), bt,
+                     bts, g.num_kv_heads, g.num_blocks, g.block_stride / per_vec,
+                     g.head_stride / per_vec, ws.items, ws.queue, num_seqs, max_ctx,
+                     bts * g.block_size, magic, sink);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+bool paged_read_supported(int cache_dtype, int head_dim, int block_size) {
+  const int eb = cache_dtype == VPA_DTYPE_FP8_E4M3 ? 1
+                 : (cache_dtype == VPA_DTYPE_BF16 || cache_dtype == VPA_DTYPE_F16) ? 2 : 0;
+  if (eb == 0 || head_dim > 128 || !cache_kernels_supported(cache_dtype, head_dim, block_size))
+    return false;
+  const int tile = head_dim * block_size * eb;
+  return tile % 1024 == 0 && tile / 1024 <= 8;
+}
+
+hipError_t launch_paged_read(int cache_dtype, const void* key_cache, const void* value_cache,
+                             const uint32_t* block_tables, int32_t block_table_stride,
+                             int32_t max_context_len, int32_t num_seqs, const CacheGeom& g,
+                             const DecodeWorkspace& ws, uint32_t magic, uint32_t* sink,
+                             hipStream_t stream) {
+  const int eb = cache_dtype == VPA_DTYPE_FP8_E4M3 ? 1 : 2;
+  const int kpl = g.head_dim * g.block_size * eb / 1024;
+#define VPA_READ_CASE(BSV, K)                                                             \
+  if (g.block_size == BSV && kpl == K)                                                     \
+    return launch_read_t<BSV, K>(key_cache, value_cache, block_tables, block_table_stride, \
+                                 max_context_len, num_seqs, g, eb, ws, magic, sink, stream);
+  VPA_READ_CASE(8, 1) VPA_READ_CASE(8, 2) VPA_READ_CASE(16, 1) VPA_READ_CASE(16, 2)
+  VPA_READ_CASE(16, 4) VPA_READ_CASE(32, 1) VPA_READ_CASE(32, 2) VPA_READ_CASE(32, 4)
+  VPA_READ_CASE(32, 8)
+#undef VPA_READ_CASE
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t max_context_len,
                               int32_t block_table_stride, int32_t num_seqs, const CacheGeom& g,

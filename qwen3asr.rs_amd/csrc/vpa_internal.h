@@ -164,6 +164,15 @@ hipError_t launch_release_blocks(const uint32_t* block_tables, int32_t cols,
                                  uint32_t* ring, uint32_t* ring_state, int32_t ring_cap,
                                  int32_t num_rows, hipStream_t stream);
 
+// The decode's read pattern with no compute (vpa_paged_cache_read): 16-bit
+// or fp8 caches, head_dim <= 128, tiles of a whole number of KiB (<= 8).
+bool paged_read_supported(int cache_dtype, int head_dim, int block_size);
+hipError_t launch_paged_read(int cache_dtype, const void* key_cache, const void* value_cache,
+                             const uint32_t* block_tables, int32_t block_table_stride,
+                             int32_t max_context_len, int32_t num_seqs, const CacheGeom& g,
+                             const DecodeWorkspace& ws, uint32_t magic, uint32_t* sink,
+                             hipStream_t stream);
+
 // True when a decode kernel is compiled for this (dtype, head_dim, block_size,
 // query heads per kv head) combination.
 bool decode_supported(int dtype, int head_dim, int block_size, int group);

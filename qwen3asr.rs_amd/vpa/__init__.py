@@ -14,6 +14,7 @@ from .ops import (  # noqa: F401
     gather_kv_cache,
     paged_attention,
     paged_attention_plan,
+    paged_cache_read,
     paged_attention_varlen_prefill,
     paged_attention_workspace,
     reshape_and_cache,
@@ -32,6 +33,7 @@ __all__ = [
     "gather_kv_cache",
     "paged_attention",
     "paged_attention_plan",
+    "paged_cache_read",
     "paged_attention_varlen_prefill",
     "paged_attention_workspace",
     "reshape_and_cache",

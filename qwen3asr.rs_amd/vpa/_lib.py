@@ -55,6 +55,8 @@ SIGNATURES = {
     "vpa_paged_attention_noalloc": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32,
                                                    _f32, _f32, _p, _i32, _i32, _i32, _i32, _i32,
                                                    _i64, _i64, _i64, _i32, _i32, _p]),
+    "vpa_paged_cache_read": (ctypes.c_int, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                            _i64, _i64, _i64, _i32, _p, _sz, _u32, _p, _p]),
     "vpa_gather_kv_cache": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _i32, _i64, _i32,
                                            _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
     "vpa_chunked_prefill_paged_attention": (ctypes.c_int, [

@@ -212,6 +212,29 @@ def paged_attention_plan(context_lens: torch.Tensor, max_context_len: int,
         workspace.numel() * workspace.element_size(), _stream(context_lens)))
 
 
+def paged_cache_read(key_cache: torch.Tensor, value_cache: torch.Tensor,
+                     block_tables: torch.Tensor, max_context_len: int, num_heads: int,
+                     workspace: torch.Tensor, sink: torch.Tensor, magic: int = 0x9E3779B9) -> None:
+    """The decode's read pattern with no compute (``vpa_paged_cache_read``):
+    every K/V byte of each sequence's context, through the work list that
+    ``paged_attention_plan`` left in ``workspace``. A measurement op: its rate
+    is the gather bandwidth the decode can reach. ``sink`` (u32 [1]) is
+    written only where a checksum equals ``magic``."""
+    _require_device(key_cache, value_cache, block_tables, workspace, sink)
+    nb, kvh, d, bs, bstride, hstride = cache_geometry(key_cache, value_cache)
+    if block_tables.dtype != torch.uint32 or block_tables.dim() != 2:
+        raise _err("block_tables must be u32 2-d")
+    if sink.dtype != torch.uint32 or sink.numel() < 1:
+        raise _err("sink must be a u32 tensor")
+    block_tables = block_tables.contiguous()
+    check(_lib.load().vpa_paged_cache_read(
+        key_cache.data_ptr(), value_cache.data_ptr(), block_tables.data_ptr(),
+        block_tables.shape[1], int(max_context_len), block_tables.shape[0], num_heads, kvh, d,
+        bs, nb, bstride, hstride, dtype_code(key_cache.dtype), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), int(magic) & 0xFFFFFFFF, sink.data_ptr(),
+        _stream(key_cache)))
+
+
 def gather_kv_cache(key_cache: torch.Tensor, value_cache: torch.Tensor,
                     k_scale: Optional[torch.Tensor], v_scale: Optional[torch.Tensor],
                     block_tables: torch.Tensor, cu_seqlens_kv: torch.Tensor,

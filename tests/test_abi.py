@@ -321,3 +321,49 @@ def test_gather_and_prefill_fp8_validation():
     assert rc == _lib.VPA_ERR_UNSUPPORTED and "differs" in msg, msg
     rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bstride=8 * 128 * 8, hstride=128 * 8)
     assert rc == _lib.VPA_ERR_UNSUPPORTED and "no MFMA kernel" in msg, msg
+
+
+def test_paged_cache_read_validation():
+    lib = _lib.load()
+
+    def call(**over):
+        a = dict(kc=FAKE, vc=FAKE, bt=FAKE, bts=64, max_ctx=1024, b=4, h=16, kvh=8, d=128, bs=16,
+                 nb=100, bstride=8 * 128 * 16, hstride=128 * 16, cdt=_lib.DTYPE_BF16, ws=None,
+                 ws_bytes=0, magic=0, sink=FAKE, stream=None)
+        a.update(over)
+        return lib.vpa_paged_cache_read(*a.values()), lib.vpa_last_error().decode()
+
+    rc, msg = call()
+    assert rc == _lib.VPA_ERR_WORKSPACE and "workspace" in msg, msg
+    rc, msg = call(cdt=_lib.DTYPE_F32, bstride=8 * 128 * 16, hstride=128 * 16)
+    assert rc == _lib.VPA_ERR_UNSUPPORTED, msg
+    rc, msg = call(bts=10)
+    assert rc == _lib.VPA_ERR_INVALID_ARGUMENT and "block_table_stride" in msg, msg
+    rc, msg = call(sink=None)
+    assert rc == _lib.VPA_ERR_INVALID_ARGUMENT and "sink" in msg, msg
+    assert call(b=0)[0] == 0
+
+
+def test_noalloc_validates_before_touching_the_device():
+    """vpa_paged_attention_noalloc runs every argument check of
+    vpa_paged_attention (same codes and messages) and its own scratch-size
+    check before it looks up its scratch on the device (there is none here)."""
+    lib = _lib.load()
+    for over in (dict(alibi=FAKE), dict(softcap=2.0), dict(h=12), dict(bts=10)):
+        args = dict(out=FAKE, q=FAKE, ks=None, vs=None, kc=FAKE, vc=FAKE, bt=FAKE, bts=64, cl=FAKE,
+                    alibi=None, max_ctx=1024, scale=0.088, softcap=1.0, sinks=None, b=4, h=16,
+                    kvh=8, d=128, bs=16, nb=100, bstride=8 * 128 * 16, hstride=128 * 16,
+                    dtype=_lib.DTYPE_BF16, cdtype=_lib.DTYPE_BF16)
+        args.update(over)
+        rc_a = lib.vpa_paged_attention(*args.values(), None, 0, None)
+        msg_a = lib.vpa_last_error().decode()
+        rc_b = lib.vpa_paged_attention_noalloc(*args.values(), None)
+        msg_b = lib.vpa_last_error().decode()
+        assert rc_a == rc_b != 0 and rc_a != _lib.VPA_ERR_WORKSPACE, msg_a
+        assert msg_b.replace("paged_attention_noalloc", "paged_attention") == msg_a
+    # 4096 sequences of 16384 tokens: 335 MB of partial rows > the 64 MiB scratch
+    rc = lib.vpa_paged_attention_noalloc(FAKE, FAKE, None, None, FAKE, FAKE, FAKE, 1024, FAKE,
+                                         None, 16384, 0.088, 1.0, None, 4096, 16, 8, 128, 16,
+                                         100, 8 * 128 * 16, 128 * 16, _lib.DTYPE_BF16,
+                                         _lib.DTYPE_BF16, None)
+    assert rc == _lib.VPA_ERR_WORKSPACE and "static scratch" in lib.vpa_last_error().decode()

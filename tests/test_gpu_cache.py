@@ -173,3 +173,36 @@ def test_gather_invalid_block_gives_zero_rows(device):
     ek, ev = orc.gather_kv_cache(kc, vc, bt, cu, dtype=code)
     np.testing.assert_array_equal(to_host(gk), ek)
     assert not to_host(gv)[16:32].any()
+
+
+def _pattern_slots(rng, pattern, t, nb, bs):
+    """Slots of t tokens: 'decode' one token per block, scattered; 'prefill'
+    runs of consecutive positions through shuffled blocks, not aligned;
+    'mixed' runs and lone tokens with padding, out-of-pool slots and tokens
+    that share a block without being neighbours."""
+    if pattern == "decode":
+        return (rng.choice(nb, size=t, replace=False).astype(np.int64) * bs
+                + rng.integers(0, bs, size=t))
+    blocks = rng.permutation(nb).astype(np.int64)
+    pos = np.arange(t) + 5
+    slots = blocks[pos // bs] * bs + pos % bs
+    if pattern == "mixed":
+        lone = rng.choice(t, size=t // 3, replace=False)
+        slots[lone] = rng.permutation(slots[lone])  # neighbours in other blocks
+        slots[::11] = -1
+        slots[7::97] = nb * bs + 3
+    return slots
+
+
+@pytest.mark.parametrize("t", [2048, 2049])
+@pytest.mark.parametrize("pattern", ["decode", "prefill", "mixed"])
+@pytest.mark.parametrize("code,bs", [(orc.BF16, 16), (orc.F32, 8), (orc.F16, 32)])
+def test_append_slot_patterns(device, t, pattern, code, bs):
+    """Large calls of each slot pattern (scattered single tokens, runs
+    through shuffled blocks, runs mixed with lone tokens, padding,
+    out-of-pool slots and tokens sharing a block without being neighbours),
+    at a whole and a ragged number of token groups: bit-exact."""
+    rng = np.random.default_rng(t + 3 * bs + code + len(pattern))
+    nb = t + 8 if pattern == "decode" else t // bs + 24
+    slots = _pattern_slots(rng, pattern, t, nb, bs)
+    run_append(device, code, 2, 128, bs, nb, slots, seed=t + bs)

@@ -304,3 +304,29 @@ def test_decode_planned_layers_match_unplanned(device, code):
     torch.cuda.synchronize()
     for i, (a, b) in enumerate(zip(got, want)):
         assert torch.equal(a, b), f"layer {i}"
+
+
+def test_paged_cache_read_reads_every_context_byte(device):
+    """vpa_paged_cache_read (the decode's reads with no compute, a measurement
+    op): over all-zero caches every lane's checksum is 0 and the sink takes
+    the magic 0; over random caches no lane's checksum is the magic and the
+    sink keeps its fill. Both after the step's plan, with multi-chunk rows."""
+    rng = np.random.default_rng(41)
+    lens = np.array([1, 17, 600, 2048, 2049, 4000], dtype=np.uint32)
+    h, kvh, d, bs = 16, 8, 128, 16
+    nb = int(((lens + bs - 1) // bs).sum()) + 8
+    bt = u32(block_tables_for(rng, lens, nb, bs), device)
+    cl = u32(lens, device)
+    ws = vpa.paged_attention_workspace(len(lens), h, d, int(lens.max()), device)
+    for fill, magic, want in ((0.0, 0, 0), (None, 0x5A5A5A5A, 0xFFFFFFFF)):
+        if fill is None:
+            kc = torch.randn((nb, kvh, d // 8, bs, 8), device=device, dtype=torch.bfloat16)
+            vc = torch.randn((nb, kvh, d, bs), device=device, dtype=torch.bfloat16)
+        else:
+            kc = torch.zeros((nb, kvh, d // 8, bs, 8), device=device, dtype=torch.bfloat16)
+            vc = torch.zeros((nb, kvh, d, bs), device=device, dtype=torch.bfloat16)
+        sink = torch.full((1,), 0xFFFFFFFF, dtype=torch.uint32, device=device)
+        vpa.paged_attention_plan(cl, int(lens.max()), bt.shape[1], h, kc, vc, torch.bfloat16, ws)
+        vpa.paged_cache_read(kc, vc, bt, int(lens.max()), h, ws, sink, magic=magic)
+        torch.cuda.synchronize()
+        assert int(sink.item()) == want

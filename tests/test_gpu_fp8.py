@@ -367,3 +367,27 @@ def test_fp8_append_then_prefill_end_to_end(device):
                                  causal=True, dtype=code, kv_dtype=orc.FP8, k_scale=ks,
                                  v_scale=vs)
     assert_attention_close(orc.to_f32(to_host(out), code), want, code, "fp8 append + prefill")
+
+
+@pytest.mark.parametrize("t", [2048, 2049])
+@pytest.mark.parametrize("pattern", ["decode", "prefill"])
+def test_fp8_append_slot_patterns(device, t, pattern):
+    """The quantising append over large calls of scattered single tokens and
+    of runs through shuffled blocks, bit-exact with the oracle."""
+    from tests.test_gpu_cache import _pattern_slots
+
+    rng = np.random.default_rng(t + len(pattern))
+    kvh, d, bs = 2, 128, 16
+    nb = t + 8 if pattern == "decode" else t // bs + 24
+    slots = _pattern_slots(rng, pattern, t, nb, bs)
+    kc = rng.integers(0, 256, size=(nb, kvh, d // 16, bs, 16), dtype=np.uint8)
+    vc = rng.integers(0, 256, size=(nb, kvh, d, bs), dtype=np.uint8)
+    k = orc.from_f32(spread_values(rng, (t, kvh, d)), orc.BF16)
+    v = orc.from_f32(spread_values(rng, (t, kvh, d)), orc.BF16)
+    kcd, vcd = f8(kc, device), f8(vc, device)
+    vpa.reshape_and_cache(to_dev(k, orc.BF16, device), to_dev(v, orc.BF16, device),
+                          scalar(0.5, device), scalar(2.0, device), kcd, vcd, i64(slots, device))
+    torch.cuda.synchronize()
+    orc.reshape_and_cache_fp8(k, v, kc, vc, slots, orc.BF16, 0.5, 2.0)
+    np.testing.assert_array_equal(f8_host(kcd), kc)
+    np.testing.assert_array_equal(f8_host(vcd), vc)
