@@ -246,9 +246,9 @@ __global__ __launch_bounds__(kThreads) void gather_kv_cache_kernel(
     const uint4* vt = reinterpret_cast<const uint4*>(value_cache + (int64_t)phys * block_stride +
                                                      head * head_stride);
     uint4* vdst = reinterpret_cast<uint4*>(v_tile);
-    for (int i = tid; i < NV; i += kThreads) {
-      k_tile[i] = kt[i];
-      vdst[i] = vt[i];
+    for (int i = tid; i < NV; i += kThreads) {  // tiles are read once: streamed
+      k_tile[i] = load_stream(kt + i);
+      vdst[i] = load_stream(vt + i);
     }
   }
   __syncthreads();
@@ -381,9 +381,9 @@ __global__ __launch_bounds__(kThreads) void gather_kv_cache_fp8_kernel(
     const uint4* kt = reinterpret_cast<const uint4*>(key_cache + off);
     const uint4* vt = reinterpret_cast<const uint4*>(value_cache + off);
     uint4* vdst = reinterpret_cast<uint4*>(v_tile);
-    for (int i = tid; i < NV; i += kThreads) {
-      k_tile[i] = kt[i];
-      vdst[i] = vt[i];
+    for (int i = tid; i < NV; i += kThreads) {  // tiles are read once: streamed
+      k_tile[i] = load_stream(kt + i);
+      vdst[i] = load_stream(vt + i);
     }
   }
   __syncthreads();

@@ -44,6 +44,16 @@ namespace {
 
 constexpr int kPT = kDecodePartitionTokens;
 
+#ifndef VPA_DECODE_STREAM_LOADS
+#define VPA_DECODE_STREAM_LOADS 1
+#endif
+// K/V tile loads of the decode: every byte is read once per call, so they
+// stream (non-temporal) unless VPA_DECODE_STREAM_LOADS is 0.
+__device__ __forceinline__ uint4 tile_load(const uint4* p) {
+  if constexpr (VPA_DECODE_STREAM_LOADS) return load_stream(p);
+  else return *p;
+}
+
 template <typename T, int D, int BS, int G>
 __global__ __launch_bounds__(64) void paged_decode_kernel(
     T* __restrict__ out, const T* __restrict__ query, const T* __restrict__ key_cache,
@@ -121,7 +131,8 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
       ok[u] = bi < nb && (int64_t)phys < num_blocks;
       const uint4* kp = kbase + (int64_t)(ok[u] ? phys : 0u) * bstride_v;
 #pragma unroll
-      for (int k = 0; k < KPL; ++k) kv[u][k] = ok[u] ? kp[lane + 64 * k] : make_uint4(0, 0, 0, 0);
+      for (int k = 0; k < KPL; ++k)
+        kv[u][k] = ok[u] ? tile_load(kp + lane + 64 * k) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -181,7 +192,8 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
       ok[u] = bi < nb && (int64_t)phys < num_blocks;
       const uint4* vp = vbase + (int64_t)(ok[u] ? phys : 0u) * bstride_v;
 #pragma unroll
-      for (int k = 0; k < KPL; ++k) vv[u][k] = ok[u] ? vp[lane + 64 * k] : make_uint4(0, 0, 0, 0);
+      for (int k = 0; k < KPL; ++k)
+        vv[u][k] = ok[u] ? tile_load(vp + lane + 64 * k) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -580,7 +592,7 @@ void paged_decode_rows_kernel(
         bool ok;
         const uint4* tp = base + (int64_t)tile_block(st, u, ok) * bstride_v + lane;
 #pragma unroll
-        for (int k = 0; k < KPL; ++k) buf[u * KPL + k] = tp[64 * k];
+        for (int k = 0; k < KPL; ++k) buf[u * KPL + k] = tile_load(tp + 64 * k);
       }
     };
     // logits of BKS tiles
@@ -1068,6 +1080,9 @@ hipError_t dispatch_decode(int dtype, int D, int BS, int group, A... args) {
   return hipErrorInvalidValue;
 }
 
+#ifndef VPA_READ_NV
+#define VPA_READ_NV 8
+#endif
 // Read ceiling of the decode's access pattern: the rows kernel's work items
 // and split of a chunk's blocks over its waves, each wave reading every K
 // then every V tile of its blocks with the same 16-byte loads (KPL per lane
@@ -1083,7 +1098,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void paged_read_kernel(
     int32_t max_ctx, int32_t cap_tokens, uint32_t magic, uint32_t* __restrict__ sink) {
   constexpr int NW = kRowsWaves;
   constexpr int PB = kRowsPT / BS;  // blocks per wave partition
-  constexpr int NV = 8;             // loads per lane per stage
+  constexpr int NV = VPA_READ_NV;    // loads per lane per stage
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const uint32_t w = blockIdx.x;
@@ -1120,7 +1135,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void paged_read_kernel(
         const int bi = v ? tile - nb : tile;
         const uint32_t phys = (uint32_t)__builtin_amdgcn_readlane((int)my_bt, bi);
         const int64_t pb = (int64_t)phys < num_blocks ? (int64_t)phys : 0;
-        buf[u] = (v ? value_cache : key_cache)[pb * block_stride_v + head_off + 64 * (i % KPL)];
+        buf[u] = tile_load((v ? value_cache : key_cache) + pb * block_stride_v + head_off +
+                           64 * (i % KPL));
       }
     }
   };
