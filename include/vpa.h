@@ -300,7 +300,9 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
  * written as zeros. n_s and L_s are clamped to max_query_len and
  * max_kv_len, which size the grid only; rows at or past total_query_rows are
  * neither read nor written. Block ids >= num_blocks are treated as absent.
- * out[row, h] = sum_t p_t V[t] / sum_t p_t (no epsilon, as flash attention).
+ * out[row, h] = sum_t p_t V[t] / (sum_t p_t + denom_eps), p_t = exp(s_t -
+ * max_t s_t): denom_eps 0 is the flash attention of the CUDA path, 1e-6 the
+ * Metal kernel (prefill_paged_attn.metal:1300); it must be finite and >= 0.
  * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 (head_dim 64 or 128,
  * block_size 16 or 32) for bf16/f16 queries: the cache is read as byte *
  * k_scale / byte * v_scale (the Metal kernel's fp8 path,
@@ -312,7 +314,7 @@ int vpa_chunked_prefill_paged_attention(
     const void* key_cache, const void* value_cache, const uint32_t* block_tables,
     int32_t block_table_stride, const uint32_t* cu_seqlens_q, const uint32_t* context_lens,
     int32_t num_seqs, int32_t max_query_len, int32_t max_kv_len, int64_t total_query_rows,
-    float softmax_scale, int32_t causal, int32_t num_heads, int32_t num_kv_heads,
+    float softmax_scale, float denom_eps, int32_t causal, int32_t num_heads, int32_t num_kv_heads,
     int32_t head_dim, int32_t block_size, int64_t num_blocks, int64_t cache_block_stride,
     int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype, void* stream);
 

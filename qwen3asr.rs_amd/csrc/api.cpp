@@ -528,11 +528,14 @@ int vpa_chunked_prefill_paged_attention(
     const void* key_cache, const void* value_cache, const uint32_t* block_tables,
     int32_t block_table_stride, const uint32_t* cu_seqlens_q, const uint32_t* context_lens,
     int32_t num_seqs, int32_t max_query_len, int32_t max_kv_len, int64_t total_query_rows,
-    float softmax_scale, int32_t causal, int32_t num_heads, int32_t num_kv_heads,
+    float softmax_scale, float denom_eps, int32_t causal, int32_t num_heads, int32_t num_kv_heads,
     int32_t head_dim, int32_t block_size, int64_t num_blocks, int64_t cache_block_stride,
     int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype, void* stream) {
   clear_error();
   const char* op = "chunked_prefill_paged_attention";
+  if (!(denom_eps >= 0.f) || denom_eps > 3.0e38f)
+    return fail(VPA_ERR_INVALID_ARGUMENT, "%s: denom_eps must be finite and >= 0, got %g", op,
+                (double)denom_eps);
   const bool fp8 = cache_dtype == VPA_DTYPE_FP8_E4M3;
   if (dtype != cache_dtype && !(fp8 && (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16)))
     return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from query dtype %s", op,
@@ -584,7 +587,8 @@ int vpa_chunked_prefill_paged_attention(
   return hip_status(op, launch_prefill_paged(dtype, cache_dtype, out, query, key_cache,
                                              value_cache, block_tables, block_table_stride,
                                              cu_seqlens_q, context_lens, num_seqs, max_query_len,
-                                             max_kv_len, total_query_rows, softmax_scale, causal,
+                                             max_kv_len, total_query_rows, softmax_scale,
+                                             denom_eps, causal,
                                              num_heads, g, fp8 ? k_scale : nullptr,
                                              fp8 ? v_scale : nullptr,
                                              static_cast<hipStream_t>(stream)));

@@ -213,9 +213,9 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     const C* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
     int32_t block_table_stride, const uint32_t* __restrict__ cu_seqlens_q,
     const uint32_t* __restrict__ context_lens, int32_t num_seqs, int32_t max_query_len,
-    int32_t max_kv_len, int64_t total_query_rows, float scale_log2, int32_t causal,
-    int32_t num_heads, int32_t num_kv_heads, int64_t num_blocks, int64_t block_stride,
-    int64_t head_stride, int32_t q_tiles, const float* __restrict__ k_scale,
+    int32_t max_kv_len, int64_t total_query_rows, float scale_log2, float denom_eps,
+    int32_t causal, int32_t num_heads, int32_t num_kv_heads, int64_t num_blocks,
+    int64_t block_stride, int64_t head_stride, int32_t q_tiles, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale) {
   constexpr bool kF8 = std::is_same_v<C, fp8_t>;
   static_assert(kF8 || std::is_same_v<C, T>, "cache type is the query type or fp8");
@@ -322,8 +322,9 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
   const float sl = fabsf(scale_log2);
-  float m = -INFINITY;  // running max of the row, log2 units
-  float lsum = 0.f;     // this lane's share of the row's exp sum
+  float m = -INFINITY;   // reference max of the row (moves lazily), log2 units
+  float mt = -INFINITY;  // the row's true max so far, log2 units
+  float lsum = 0.f;      // this lane's share of the row's exp sum
 
   const C* kbase = key_cache + (int64_t)j * head_stride;
   const C* vbase = value_cache + (int64_t)j * head_stride;
@@ -561,6 +562,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
     mx = max_xor32(mx) * sl;
+    mt = fmaxf(mt, mx);
     // The reference max m only moves when some row's step max exceeds it by
     // more than kRescaleSlack (log2 units): the probabilities stay below
     // 2^kRescaleSlack, and O and the row sums are rescaled only then.
@@ -645,8 +647,14 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     }
   }
 
+  // the denominator's epsilon is relative to the row's true max: the sums
+  // here are relative to m, 2^(mt - m) (at most 2^kRescaleSlack) times
+  // larger
   const float total = sum_xor32(lsum);
-  const float inv = total > 0.f ? vs / total : 0.f;  // a row that sees no key gives 0
+  const float eps_m = denom_eps > 0.f && m != -INFINITY
+                          ? denom_eps * __builtin_amdgcn_exp2f(mt - m)
+                          : 0.f;
+  const float inv = total > 0.f ? vs / (total + eps_m) : 0.f;  // a row that sees no key gives 0
   if (row_ok) {
     T* orow = out + (row * num_heads + head) * D;
 #pragma unroll
@@ -674,6 +682,7 @@ struct PrefillArgs {
   int32_t num_seqs, max_query_len, max_kv_len;
   int64_t total_query_rows;
   float scale;
+  float denom_eps;
   int32_t causal, num_heads;
   const float* k_scale;
   const float* v_scale;
@@ -691,7 +700,8 @@ hipError_t launch_prefill_t(const PrefillArgs& a, const CacheGeom& g, hipStream_
                      static_cast<const T*>(a.query), static_cast<const C*>(a.key_cache),
                      static_cast<const C*>(a.value_cache), a.block_tables, a.block_table_stride,
                      a.cu_seqlens_q, a.context_lens, a.num_seqs, a.max_query_len, a.max_kv_len,
-                     a.total_query_rows, scale_log2, a.causal, a.num_heads, g.num_kv_heads,
+                     a.total_query_rows, scale_log2, a.denom_eps, a.causal, a.num_heads,
+                     g.num_kv_heads,
                      g.num_blocks, g.block_stride, g.head_stride, q_tiles, a.k_scale,
                      a.v_scale);
   return hipGetLastError();
@@ -753,14 +763,16 @@ hipError_t launch_prefill_paged(int dtype, int cache_dtype, void* out, const voi
                                 const uint32_t* block_tables, int32_t block_table_stride,
                                 const uint32_t* cu_seqlens_q, const uint32_t* context_lens,
                                 int32_t num_seqs, int32_t max_query_len, int32_t max_kv_len,
-                                int64_t total_query_rows, float scale, int32_t causal,
-                                int32_t num_heads, const CacheGeom& g, const float* k_scale,
-                                const float* v_scale, hipStream_t stream) {
+                                int64_t total_query_rows, float scale, float denom_eps,
+                                int32_t causal, int32_t num_heads, const CacheGeom& g,
+                                const float* k_scale, const float* v_scale,
+                                hipStream_t stream) {
   const int group = num_heads / g.num_kv_heads;
   const PrefillArgs a{out,       query,        key_cache,      value_cache,  block_tables,
                       block_table_stride,      cu_seqlens_q,   context_lens, num_seqs,
                       max_query_len,           max_kv_len,     total_query_rows,
-                      scale,     causal,       num_heads,      k_scale,      v_scale};
+                      scale,     denom_eps,    causal,         num_heads,    k_scale,
+                      v_scale};
   const bool f8 = cache_dtype == VPA_DTYPE_FP8_E4M3;
   if (dtype == VPA_DTYPE_BF16)
     return f8 ? dispatch_shape<bf16_t, fp8_t>(group, a, g, stream)

@@ -121,9 +121,10 @@ hipError_t launch_prefill_paged(int dtype, int cache_dtype, void* out, const voi
                                 const uint32_t* block_tables, int32_t block_table_stride,
                                 const uint32_t* cu_seqlens_q, const uint32_t* context_lens,
                                 int32_t num_seqs, int32_t max_query_len, int32_t max_kv_len,
-                                int64_t total_query_rows, float scale, int32_t causal,
-                                int32_t num_heads, const CacheGeom& g, const float* k_scale,
-                                const float* v_scale, hipStream_t stream);
+                                int64_t total_query_rows, float scale, float denom_eps,
+                                int32_t causal, int32_t num_heads, const CacheGeom& g,
+                                const float* k_scale, const float* v_scale,
+                                hipStream_t stream);
 
 // Query positions one prefill workgroup covers for a GQA group size.
 int prefill_positions_per_workgroup(int group);

@@ -60,8 +60,8 @@ SIGNATURES = {
     "vpa_gather_kv_cache": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _i32, _i64, _i32,
                                            _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
     "vpa_chunked_prefill_paged_attention": (ctypes.c_int, [
-        _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i64, _f32, _i32, _i32,
-        _i32, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
+        _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i64, _f32, _f32, _i32,
+        _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
     "vpa_argmax_rows": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p]),
     "vpa_decode_consume_tokens": (ctypes.c_int, [
         _p, _p, _p, _p, _p, _i32, _p, _i32, _u32, _p, _p, _i32, _p]),

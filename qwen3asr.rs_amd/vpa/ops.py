@@ -274,7 +274,8 @@ def paged_attention_varlen_prefill(q: torch.Tensor, key_cache: torch.Tensor,
                                    scale: float, softcapping: float, *, causal: bool = False,
                                    max_query_len: Optional[int] = None,
                                    max_context_len: Optional[int] = None,
-                                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                                   out: Optional[torch.Tensor] = None,
+                                   denom_eps: Optional[float] = None) -> torch.Tensor:
     """Varlen prefill attention of packed queries over the paged cache.
 
     Argument order and meaning follow the reference's Metal op
@@ -285,7 +286,10 @@ def paged_attention_varlen_prefill(q: torch.Tensor, key_cache: torch.Tensor,
     sequence s owns rows cu_seqlens_q[s]..cu_seqlens_q[s+1]-1 and the first
     context_lens[s] cached tokens (its own new tokens included). The maxima
     size the grid; a caller that knows them on the host passes them to skip
-    a device read. Returns [total_q, H, D]."""
+    a device read. ``denom_eps`` is added to the softmax denominator; by
+    default 1e-6 without ``causal`` (the Metal kernel,
+    ``prefill_paged_attn.metal:1300``) and 0 with it (flash attention).
+    Returns [total_q, H, D]."""
     _require_device(q, key_cache, value_cache, block_tables, context_lens, cu_seqlens_q)
     nb, kvh, d, bs, bstride, hstride = cache_geometry(key_cache, value_cache)
     if softcapping != 1.0:
@@ -320,7 +324,9 @@ def paged_attention_varlen_prefill(q: torch.Tensor, key_cache: torch.Tensor,
         out.data_ptr(), q.data_ptr(), _ptr(k_scale), _ptr(v_scale), key_cache.data_ptr(),
         value_cache.data_ptr(), block_tables.data_ptr(), block_tables.shape[1],
         cu_seqlens_q.data_ptr(), context_lens.data_ptr(), num_seqs, int(max_query_len),
-        int(max_context_len), tq, float(scale), int(bool(causal)), h, kvh, d, bs, nb, bstride,
+        int(max_context_len), tq, float(scale),
+        float((0.0 if causal else 1e-6) if denom_eps is None else denom_eps), int(bool(causal)),
+        h, kvh, d, bs, nb, bstride,
         hstride, dtype_code(q.dtype), dtype_code(key_cache.dtype), _stream(q)))
     return out
 

@@ -174,7 +174,8 @@ def test_gather_host_validation():
 
 def pf_call(**over):
     args = dict(out=FAKE, q=FAKE, ks=None, vs=None, kc=FAKE, vc=FAKE, bt=FAKE, bts=64,
-                cuq=FAKE, cl=FAKE, b=4, maxq=512, maxkv=1024, tq=2048, scale=0.088, causal=1,
+                cuq=FAKE, cl=FAKE, b=4, maxq=512, maxkv=1024, tq=2048, scale=0.088, eps=0.0,
+                causal=1,
                 h=16, kvh=8, d=128, bs=16, nb=100, bstride=8 * 128 * 16, hstride=128 * 16,
                 dtype=_lib.DTYPE_BF16, cdtype=_lib.DTYPE_BF16, stream=None)
     args.update(over)

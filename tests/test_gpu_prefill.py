@@ -273,3 +273,38 @@ def test_prefill_matches_gather_then_dense_attention(device):
                                                                 scale=d ** -0.5)
         g = got[cu_q[s]:cu_q[s + 1]].transpose(0, 1)
         assert_attention_close(g.numpy(), want.numpy(), code, f"two-pass seq {s}")
+
+
+@pytest.mark.parametrize("eps", [1e-6, 0.5, 3.0])
+@pytest.mark.parametrize("causal", [False, True])
+def test_prefill_denominator_epsilon(device, eps, causal):
+    """denom_eps is added to the softmax denominator relative to the row's
+    true max (1e-6 is the Metal kernel's, prefill_paged_attn.metal:1300).
+    Large values move the output far beyond the tolerance, so a missing or
+    mis-scaled epsilon fails; a large softmax scale makes the kernel's
+    reference max trail the true max so the rescaling of the epsilon is
+    exercised."""
+    rng = np.random.default_rng(int(eps * 100) + causal)
+    code, h, kvh, d, bs = orc.BF16, 16, 8, 128, 16
+    prior, qlens = np.array([40, 0, 300]), np.array([70, 33, 129])
+    lens = prior + qlens
+    nb = int(((lens + bs - 1) // bs).sum()) + 8
+    kc, vc = make_cache(rng, nb, kvh, d, bs, code)
+    bt = block_tables_for(rng, lens, nb, bs)
+    q = random_words(rng, (int(qlens.sum()), h, d), code)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.uint32)
+    for scale in (d ** -0.5, 2.0):
+        out = vpa.paged_attention_varlen_prefill(
+            to_dev(q, code, device), to_dev(kc, code, device), to_dev(vc, code, device),
+            u32(bt, device), u32(lens, device), u32(cu, device), None, None, scale, 1.0,
+            causal=causal, denom_eps=eps)
+        torch.cuda.synchronize()
+        want = orc.prefill_attention(q, kc, vc, bt, lens.astype(np.uint32), cu, scale,
+                                     causal=causal, dtype=code, eps=eps)
+        assert_attention_close(orc.to_f32(to_host(out), code), want, code,
+                               f"eps={eps} causal={causal} scale={scale}")
+    if eps >= 0.5:  # the epsilon matters at this size: eps = 0 is far off
+        none = orc.prefill_attention(q, kc, vc, bt, lens.astype(np.uint32), cu, scale,
+                                     causal=causal, dtype=code, eps=0.0)
+        err = np.abs(orc.to_f32(to_host(out), code) - none).max() / np.abs(none).max()
+        assert err > 0.05
