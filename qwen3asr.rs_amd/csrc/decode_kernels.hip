@@ -74,6 +74,12 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
   static_assert(PB <= 64, "block-table slice must fit one wave");
 
   __shared__ float s_p[G][kPT];
+  // Shapes whose query vectors would not fit registers (G x KPL > 16, e.g.
+  // f32 at head_dim 256 with 32-token blocks: 128 vectors per lane) read
+  // them from LDS at each use instead.
+  constexpr bool kQinLds = G * KPL > 16;
+  constexpr int CHQ = D / X;  // 16-byte chunks of a query row
+  __shared__ uint4 s_q[kQinLds ? G * CHQ : 1];
 
   const int lane = threadIdx.x;
   const int j = blockIdx.x;  // kv head
@@ -101,10 +107,18 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
   const uint32_t* bt_row = block_tables + (int64_t)s * block_table_stride;
   const uint32_t my_bt = lane < nb ? bt_row[b_begin + lane] : 0u;
 
-  // Query chunks this lane multiplies against in the key tile.
-  uint4 qv[G][KPL];
-  {
-    const int c0 = lane / BS;
+  // Query chunks this lane multiplies against in the key tile: chunk
+  // lane / BS + k * LPT of each head, in registers or (kQinLds) in LDS.
+  uint4 qv[kQinLds ? 1 : G][kQinLds ? 1 : KPL];
+  const int c0 = lane / BS;
+  if constexpr (kQinLds) {
+    for (int i = lane; i < G * CHQ; i += 64) {
+      const int g = i / CHQ, c = i - g * CHQ;
+      s_q[i] = *reinterpret_cast<const uint4*>(query + ((int64_t)s * num_heads + j * G + g) * D +
+                                                c * X);
+    }
+    lds_wave_sync();
+  } else {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const T* qrow = query + ((int64_t)s * num_heads + j * G + g) * D;
@@ -113,6 +127,10 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
         qv[g][k] = *reinterpret_cast<const uint4*>(qrow + (c0 + k * LPT) * X);
     }
   }
+  auto qchunk = [&](int g, int k) -> uint4 {
+    if constexpr (kQinLds) return s_q[g * CHQ + c0 + k * LPT];
+    else return qv[g][k];
+  };
 
   const int64_t head_off = (int64_t)j * head_stride;
   const uint4* kbase = reinterpret_cast<const uint4*>(key_cache + head_off);
@@ -144,7 +162,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
         for (int g = 0; g < G; ++g) {
           float acc = 0.f;
 #pragma unroll
-          for (int k = 0; k < KPL; ++k) acc = dot16<T>(qv[g][k], kv[u][k], acc);
+          for (int k = 0; k < KPL; ++k) acc = dot16<T>(qchunk(g, k), kv[u][k], acc);
           acc = wave_sum_range<BS, 32>(acc);
           const float logit = valid ? acc * scale : -INFINITY;
           if (lane < BS) s_p[g][bi * BS + lane] = logit;

@@ -380,10 +380,14 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
       for (int i = 0; i < DPW; ++i) {
         const int di = wave * DPW + i;  // uniform
         const int b = di / DPB;
-        uint32_t phys = pb[0];
-#pragma unroll
-        for (int k = 1; k < NBT; ++k)
-          if (b == k) phys = pb[k];
+        uint32_t phys;
+        if constexpr (NBT <= 2) {
+          phys = b == 0 ? pb[0] : pb[NBT - 1];
+        } else {
+          // (a select over more blocks by the runtime index b becomes an
+          // indexed scratch array: load the id from the table instead)
+          phys = bt[__builtin_amdgcn_readfirstlane(min(k0 / BS + b, last_blk))];
+        }
         phys = (k0 + b * BS < k_len && (int64_t)phys < num_blocks) ? phys : 0u;
         phys = __builtin_amdgcn_readfirstlane(phys);
         const int64_t blk = (int64_t)phys * block_stride;
