@@ -74,6 +74,12 @@ const char* vpa_version(void);
  * blocks. Restates PagedKvCache::new_inner (paged_kv_cache.rs:229-314):
  * x = 16 / dtype_bytes, head_dim must be a multiple of x, every size
  * non-zero. Fills key_shape[5] and value_shape[4].
+ *
+ * The ops below take head_dim 64, 96, 128, 192 or 256 and block_size 8, 16
+ * or 32 (the append and the gather every combination; decode and prefill
+ * need a (block, head) tile of a whole number of KiB, head_dim * block_size
+ * / x a multiple of 64, so head_dim 96 needs 16- or 32-token blocks at 16
+ * bits and 32-token blocks at fp8). Other shapes return VPA_ERR_UNSUPPORTED.
  */
 int vpa_cache_layout(int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                      int64_t num_blocks, int32_t cache_dtype, int64_t* key_shape,
@@ -303,8 +309,12 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
  * out[row, h] = sum_t p_t V[t] / (sum_t p_t + denom_eps), p_t = exp(s_t -
  * max_t s_t): denom_eps 0 is the flash attention of the CUDA path, 1e-6 the
  * Metal kernel (prefill_paged_attn.metal:1300); it must be finite and >= 0.
- * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 (head_dim 64 or 128,
- * block_size 16 or 32) for bf16/f16 queries: the cache is read as byte *
+ * Head dims 64, 96, 128, 192 and 256 (the Metal kernel's set,
+ * varlen_prefill.rs:15), 1, 2 or 4 query heads per kv head.
+ * cache_dtype equals dtype (block_size 8, 16 or 32), or is
+ * VPA_DTYPE_FP8_E4M3 (block_size 16 or 32) for bf16/f16 queries; head_dim 96
+ * needs 16- or 32-token blocks at 16 bits and 32-token blocks at fp8. The
+ * cache is read as byte *
  * k_scale / byte * v_scale (the Metal kernel's fp8 path,
  * prefill_paged_attn.metal:698-769), converted to the query type in
  * registers. Needs no workspace; safe under stream capture.

@@ -99,7 +99,7 @@ int check_cache(const char* op, int32_t cache_dtype, int32_t num_kv_heads, int32
   if (!cache_kernels_supported(cache_dtype, head_dim, block_size))
     return fail(VPA_ERR_UNSUPPORTED,
                 "%s: no kernel for dtype=%s head_dim=%d block_size=%d (head_dim in "
-                "{64,128,256}, block_size in {8,16,32})",
+                "{64,96,128,192,256}, block_size in {8,16,32})",
                 op, dtype_name(cache_dtype), head_dim, block_size);
   const int64_t tile = (int64_t)head_dim * block_size;
   if (head_stride < tile || block_stride < head_stride * num_kv_heads)
@@ -285,9 +285,15 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: num_heads=%d not a multiple of num_kv_heads=%d",
                 op, num_heads, num_kv_heads);
   const int group = num_heads / num_kv_heads;
-  if (!decode_supported(dtype, head_dim, block_size, group))
+  if (!(group == 1 || group == 2 || group == 4))
     return fail(VPA_ERR_UNSUPPORTED,
                 "%s: no kernel for %d query heads per kv head (supported: 1, 2, 4)", op, group);
+  if (!decode_supported(dtype, head_dim, block_size, group))
+    return fail(VPA_ERR_UNSUPPORTED,
+                "%s: no decode kernel for %s head_dim=%d block_size=%d (a (block, head) tile "
+                "must be a multiple of 1 KiB: head_dim 96 needs 16- or 32-token blocks at "
+                "16 bits)",
+                op, dtype_name(dtype), head_dim, block_size);
   if (max_context_len > kDecodeMaxPartitions * kDecodeMinPartitionTokens)
     return fail(VPA_ERR_UNSUPPORTED, "%s: max_context_len=%d exceeds %d", op, max_context_len,
                 kDecodeMaxPartitions * kDecodeMinPartitionTokens);
@@ -559,8 +565,9 @@ int vpa_chunked_prefill_paged_attention(
   if (!prefill_supported(dtype, cache_dtype, head_dim, block_size, group))
     return fail(VPA_ERR_UNSUPPORTED,
                 "%s: no MFMA kernel for dtype=%s cache=%s head_dim=%d block_size=%d group=%d "
-                "(bf16/f16, head_dim 64/128, block_size 8/16/32, 1/2/4 query heads per kv "
-                "head; fp8 caches: head_dim 64/128, block_size 16/32)",
+                "(bf16/f16, head_dim 64/96/128/192/256, block_size 8/16/32, 1/2/4 query "
+                "heads per kv head; fp8 caches: block_size 16/32; head_dim 96 needs "
+                "16- or 32-token blocks at 16 bits and 32-token blocks at fp8)",
                 op, dtype_name(dtype), dtype_name(cache_dtype), head_dim, block_size, group);
   if (num_seqs == 0 || max_query_len == 0 || total_query_rows == 0) return VPA_OK;
   {

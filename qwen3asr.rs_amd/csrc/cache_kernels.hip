@@ -489,6 +489,12 @@ hipError_t dispatch_cache(int dtype, int D, int BS, A&&... args);
   if (D == 128 && BS == 8) return FN<T, 128, 8>(args...); \
   if (D == 128 && BS == 16) return FN<T, 128, 16>(args...); \
   if (D == 128 && BS == 32) return FN<T, 128, 32>(args...); \
+  if (D == 96 && BS == 8) return FN<T, 96, 8>(args...);   \
+  if (D == 96 && BS == 16) return FN<T, 96, 16>(args...); \
+  if (D == 96 && BS == 32) return FN<T, 96, 32>(args...); \
+  if (D == 192 && BS == 8) return FN<T, 192, 8>(args...); \
+  if (D == 192 && BS == 16) return FN<T, 192, 16>(args...); \
+  if (D == 192 && BS == 32) return FN<T, 192, 32>(args...); \
   if (D == 256 && BS == 8) return FN<T, 256, 8>(args...); \
   if (D == 256 && BS == 16) return FN<T, 256, 16>(args...); \
   if (D == 256 && BS == 32) return FN<T, 256, 32>(args...);
@@ -523,7 +529,8 @@ hipError_t dispatch_gather(int dtype, int D, int BS, A... args) {
 bool cache_kernels_supported(int dtype, int head_dim, int block_size) {
   const bool dt = dtype == VPA_DTYPE_F32 || dtype == VPA_DTYPE_BF16 ||
                   dtype == VPA_DTYPE_F16 || dtype == VPA_DTYPE_FP8_E4M3;
-  const bool d = head_dim == 64 || head_dim == 128 || head_dim == 256;
+  const bool d = head_dim == 64 || head_dim == 96 || head_dim == 128 || head_dim == 192 ||
+                 head_dim == 256;
   const bool bs = block_size == 8 || block_size == 16 || block_size == 32;
   return dt && d && bs;
 }

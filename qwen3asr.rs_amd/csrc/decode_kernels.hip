@@ -1,10 +1,10 @@
 // Paged-attention decode for gfx950, two paths:
-//   * 16-bit and fp8 caches with head_dim <= 128 (vASR's shapes): a work
+//   * 16-bit and fp8 caches with head_dim 64 or 128 (vASR's shapes): a work
 //     list built on the device (decode_plan_kernel, longest chunk first),
 //     paged_decode_rows_kernel (one workgroup per (chunk, kv head), its
 //     waves splitting the chunk's blocks) and decode_merge_kernel for the
 //     sequences longer than one chunk; described further down;
-//   * f32 caches and head_dim 256: paged_decode_kernel, one wavefront per
+//   * f32 caches and head_dim 96, 192, 256: paged_decode_kernel, one wavefront per
 //     (kv head, sequence, split-K partition of kDecodePartitionTokens
 //     tokens) serving all the query heads of that kv head (GQA), and
 //     paged_decode_reduce_kernel merging the partitions; described here.
@@ -1047,8 +1047,9 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (group == 2) return launch_decode_rows<T, D, BS, 2>(args...);   \
   if (group == 4) return launch_decode_rows<T, D, BS, 4>(args...);
 
-// 16-bit caches with head_dim <= 128 use the rows kernel; f32 and
-// head_dim 256 use the generic kernel.
+// 16-bit caches with head_dim 64 or 128 use the rows kernel; f32 and the
+// other head dims the generic kernel (head_dim 96 at 16-bit needs blocks of
+// 16 or 32 tokens: a (block, head) tile is a whole number of 1 KiB wave loads).
 #define VPA_DECODE_DBS16(T)                                   \
   if (D == 64 && BS == 8) { VPA_DECODE_ROWS_G(T, 64, 8) }     \
   if (D == 64 && BS == 16) { VPA_DECODE_ROWS_G(T, 64, 16) }   \
@@ -1056,6 +1057,11 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (D == 128 && BS == 8) { VPA_DECODE_ROWS_G(T, 128, 8) }   \
   if (D == 128 && BS == 16) { VPA_DECODE_ROWS_G(T, 128, 16) } \
   if (D == 128 && BS == 32) { VPA_DECODE_ROWS_G(T, 128, 32) } \
+  if (D == 96 && BS == 16) { VPA_DECODE_G(T, 96, 16) }        \
+  if (D == 96 && BS == 32) { VPA_DECODE_G(T, 96, 32) }        \
+  if (D == 192 && BS == 8) { VPA_DECODE_G(T, 192, 8) }        \
+  if (D == 192 && BS == 16) { VPA_DECODE_G(T, 192, 16) }      \
+  if (D == 192 && BS == 32) { VPA_DECODE_G(T, 192, 32) }      \
   if (D == 256 && BS == 8) { VPA_DECODE_G(T, 256, 8) }        \
   if (D == 256 && BS == 16) { VPA_DECODE_G(T, 256, 16) }      \
   if (D == 256 && BS == 32) { VPA_DECODE_G(T, 256, 32) }
@@ -1067,6 +1073,12 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (D == 128 && BS == 8) { VPA_DECODE_G(T, 128, 8) }      \
   if (D == 128 && BS == 16) { VPA_DECODE_G(T, 128, 16) }    \
   if (D == 128 && BS == 32) { VPA_DECODE_G(T, 128, 32) }    \
+  if (D == 96 && BS == 8) { VPA_DECODE_G(T, 96, 8) }        \
+  if (D == 96 && BS == 16) { VPA_DECODE_G(T, 96, 16) }      \
+  if (D == 96 && BS == 32) { VPA_DECODE_G(T, 96, 32) }      \
+  if (D == 192 && BS == 8) { VPA_DECODE_G(T, 192, 8) }      \
+  if (D == 192 && BS == 16) { VPA_DECODE_G(T, 192, 16) }    \
+  if (D == 192 && BS == 32) { VPA_DECODE_G(T, 192, 32) }    \
   if (D == 256 && BS == 8) { VPA_DECODE_G(T, 256, 8) }      \
   if (D == 256 && BS == 16) { VPA_DECODE_G(T, 256, 16) }    \
   if (D == 256 && BS == 32) { VPA_DECODE_G(T, 256, 32) }
@@ -1197,7 +1209,8 @@ hipError_t launch_read_t(const void* kc, const void* vc, const uint32_t* bt, int
 bool paged_read_supported(int cache_dtype, int head_dim, int block_size) {
   const int eb = cache_dtype == VPA_DTYPE_FP8_E4M3 ? 1
                  : (cache_dtype == VPA_DTYPE_BF16 || cache_dtype == VPA_DTYPE_F16) ? 2 : 0;
-  if (eb == 0 || head_dim > 128 || !cache_kernels_supported(cache_dtype, head_dim, block_size))
+  if (eb == 0 || !(head_dim == 64 || head_dim == 128) ||
+      !cache_kernels_supported(cache_dtype, head_dim, block_size))
     return false;
   const int tile = head_dim * block_size * eb;
   return tile % 1024 == 0 && tile / 1024 <= 8;
@@ -1224,7 +1237,7 @@ hipError_t launch_paged_read(int cache_dtype, const void* key_cache, const void*
 hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t max_context_len,
                               int32_t block_table_stride, int32_t num_seqs, const CacheGeom& g,
                               const DecodeWorkspace& ws, hipStream_t stream) {
-  const bool rows = (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) && g.head_dim <= 128;
+  const bool rows = decode_uses_rows_kernel(dtype, g.head_dim);
   if (!rows || num_seqs == 0) return hipSuccess;
   hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, context_lens, num_seqs,
                      max_context_len, block_table_stride * g.block_size, kDecodeChunk, ws.items,
@@ -1233,8 +1246,14 @@ hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t m
 }
 
 bool decode_supported(int dtype, int head_dim, int block_size, int group) {
-  return cache_kernels_supported(dtype, head_dim, block_size) &&
-         (group == 1 || group == 2 || group == 4);
+  const int x = dtype == VPA_DTYPE_F32 ? 4 : 8;
+  return dtype != VPA_DTYPE_FP8_E4M3 && cache_kernels_supported(dtype, head_dim, block_size) &&
+         (head_dim * block_size / x) % 64 == 0 && (group == 1 || group == 2 || group == 4);
+}
+
+bool decode_uses_rows_kernel(int dtype, int head_dim) {
+  return (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) &&
+         (head_dim == 64 || head_dim == 128);
 }
 
 namespace {
@@ -1263,8 +1282,7 @@ WorkspacePlan plan_workspace(int num_seqs, int num_heads, int head_dim, int max_
 }  // namespace
 
 int decode_part_tokens(int dtype, int head_dim) {
-  const bool rows = (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) && head_dim <= 128;
-  return rows ? kDecodeChunk : kPT;
+  return decode_uses_rows_kernel(dtype, head_dim) ? kDecodeChunk : kPT;
 }
 
 size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len,

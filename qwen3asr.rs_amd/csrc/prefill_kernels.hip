@@ -206,9 +206,57 @@ __device__ __forceinline__ constexpr int tile_key_of_row(int i) {
   return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
 }
 
+// s_waitcnt lgkmcnt(0) that the N registers just read from LDS (by the inline
+// ds_read above) depend on. At the head dims 64 and 128 the wait names them
+// all; otherwise it names the first few and an empty statement per other
+// register keeps every later use of it behind the wait.
+template <typename V, int N>
+__device__ __forceinline__ void lgkm_wait(V (&r)[N]) {
+  if constexpr (N == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+  } else if constexpr (N == 8) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
+                 "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
+  } else {
+    static_assert(N > 4, "operand count");
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+#pragma unroll
+    for (int i = 4; i < N; ++i) asm volatile("" : "+v"(r[i]));
+  }
+}
+template <typename V, int N>
+__device__ __forceinline__ void lgkm_wait(V (&r)[N][2]) {
+  if constexpr (N == 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0][0]), "+v"(r[0][1]), "+v"(r[1][0]), "+v"(r[1][1]));
+  } else if constexpr (N == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0][0]), "+v"(r[0][1]), "+v"(r[1][0]), "+v"(r[1][1]), "+v"(r[2][0]),
+                   "+v"(r[2][1]), "+v"(r[3][0]), "+v"(r[3][1]));
+  } else {
+    static_assert(N == 3 || N > 4, "operand count");
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0][0]), "+v"(r[0][1]), "+v"(r[1][0]), "+v"(r[1][1]), "+v"(r[2][0]),
+                   "+v"(r[2][1]));
+#pragma unroll
+    for (int i = 3; i < N; ++i) {
+      asm volatile("" : "+v"(r[i][0]));
+      asm volatile("" : "+v"(r[i][1]));
+    }
+  }
+}
+
+// Waves per SIMD the kernel is built for: two up to head_dim 128; above,
+// the accumulators and operands of a 32-row wave (O alone is D / 2 VGPRs)
+// need the whole register file of one wave.
+template <int D>
+constexpr int prefill_waves_per_eu() {
+  return D > 128 ? 1 : VPA_PREFILL_WAVES_PER_EU;
+}
+
 template <typename T, typename C, int D, int BS, int G>
 __global__ __launch_bounds__(kPrefillThreads)
-__attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_paged_kernel(
+__attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_paged_kernel(
     T* __restrict__ out, const T* __restrict__ query, const C* __restrict__ key_cache,
     const C* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
     int32_t block_table_stride, const uint32_t* __restrict__ cu_seqlens_q,
@@ -229,9 +277,10 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   constexpr int DT = D / 32;    // 32-row tiles of O^T
   constexpr int UB = BS / X;    // 16-byte units per value row of a block
   constexpr int NU = D * KT / X;                   // 16-byte units per K (and per V) tile
+  constexpr int NDMA = NU / 64;                    // DMAs per K (and per V) tile
   // DMAs per issuing wave per K (and per V) tile; the first DMW waves issue
-  constexpr int DPW = NU >= kPrefillThreads ? NU / kPrefillThreads : 1;
-  constexpr int DMW = NU / 64 / DPW;
+  constexpr int DPW = (NDMA + kPrefillWaves - 1) / kPrefillWaves;
+  constexpr int DMW = NDMA / DPW;
   constexpr int DPT = 2 * DPW;                     // DMAs per wave per tile
   constexpr int NBT = KT / BS;                     // blocks per tile
   constexpr int RBV = D * UB;                      // units of one block's K (or V) rows
@@ -240,7 +289,7 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
   // lanes of one LDS read pass span two blocks, padded to other banks
   constexpr int RBK = RBV + (BS == 8 ? 8 : 0);
   constexpr int KU = NBT * RBK;                    // K units of a stage
-  static_assert(KT % BS == 0 && BS >= 8 && NU % 64 == 0 && DMW * DPW * 64 == NU &&
+  static_assert(KT % BS == 0 && BS >= 8 && NU % 64 == 0 && DMW * DPW == NDMA &&
                     DMW <= kPrefillWaves && RBV % 64 == 0 && (DMW * DPW) % DPB == 0,
                 "tile shape");
 
@@ -453,26 +502,13 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
     if constexpr (kF8) {
       v2i_t k8[KS];
       lds_read_seq8<BS * 16>(k8, ka_lane + lds_addr(sk), std::make_integer_sequence<int, KS>{});
-      if constexpr (KS == 8) {
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k8[0]), "+v"(k8[1]), "+v"(k8[2]), "+v"(k8[3]),
-                     "+v"(k8[4]), "+v"(k8[5]), "+v"(k8[6]), "+v"(k8[7]));
-      } else {
-        static_assert(KS == 4, "head_dim 64 or 128");
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k8[0]), "+v"(k8[1]), "+v"(k8[2]), "+v"(k8[3]));
-      }
+      lgkm_wait(k8);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kop[ks] = fp8x8_operand<T>(k8[ks]);
-    } else if constexpr (KS == 8) {
-      lds_read_seq<2 * BS * 16>(kop, ka_lane + lds_addr(sk),
-                                std::make_integer_sequence<int, KS>{});
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kop[0]), "+v"(kop[1]), "+v"(kop[2]),
-                   "+v"(kop[3]), "+v"(kop[4]), "+v"(kop[5]), "+v"(kop[6]), "+v"(kop[7]));
     } else {
-      static_assert(KS == 4, "head_dim 64 or 128");
       lds_read_seq<2 * BS * 16>(kop, ka_lane + lds_addr(sk),
                                 std::make_integer_sequence<int, KS>{});
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kop[0]), "+v"(kop[1]), "+v"(kop[2]),
-                   "+v"(kop[3]));
+      lgkm_wait(kop);
     }
     f32x16_t sacc = s_tile_mfma<T, KS>(kop, qop);
     if (!full) {
@@ -512,31 +548,15 @@ __attribute__((amdgpu_waves_per_eu(VPA_PREFILL_WAVES_PER_EU))) void prefill_page
       v2i_t v8[DT][2];
       lds_read_pairs8<32 * 16, kVStep1>(v8, va_lane + lds_addr(sv),
                                         std::make_integer_sequence<int, DT>{});
-      if constexpr (DT == 4) {
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(v8[0][0]), "+v"(v8[0][1]), "+v"(v8[1][0]), "+v"(v8[1][1]),
-                       "+v"(v8[2][0]), "+v"(v8[2][1]), "+v"(v8[3][0]), "+v"(v8[3][1]));
-      } else {
-        static_assert(DT == 2, "head_dim 64 or 128");
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(v8[0][0]), "+v"(v8[0][1]), "+v"(v8[1][0]), "+v"(v8[1][1]));
-      }
+      lgkm_wait(v8);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) vop[dt][k2] = fp8x8_operand<T>(v8[dt][k2]);
-    } else if constexpr (DT == 4) {
-      lds_read_pairs<32 * 16, kVStep1>(vop, va_lane + lds_addr(sv),
-                                       std::make_integer_sequence<int, DT>{});
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[1][0]), "+v"(vop[1][1]),
-                     "+v"(vop[2][0]), "+v"(vop[2][1]), "+v"(vop[3][0]), "+v"(vop[3][1]));
     } else {
-      static_assert(DT == 2, "head_dim 64 or 128");
       lds_read_pairs<32 * 16, kVStep1>(vop, va_lane + lds_addr(sv),
                                        std::make_integer_sequence<int, DT>{});
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(vop[0][0]), "+v"(vop[0][1]), "+v"(vop[1][0]), "+v"(vop[1][1]));
+      lgkm_wait(vop);
     }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -726,26 +746,50 @@ hipError_t dispatch_group(int group, const PrefillArgs& a, const CacheGeom& g,
   }
 }
 
-// fp8 caches: head_dim 64 or 128, block_size 16 or 32 (at head_dim 128 a
-// 32-key tile is 256 16-byte units, one DMA per lane of the workgroup; at 64,
-// 128 units moved by two of the four waves)
+// Shapes: head_dim 64, 96, 128, 192 or 256 with a (block, head) tile of a
+// whole number of 1 KiB DMAs (D * BS / x a multiple of 64 units): 16-bit
+// caches at block sizes 8, 16, 32 (head_dim 96 at 16 and 32); fp8 caches at
+// 16 and 32 (head_dim 96 at 32). At fp8 head_dim 64 a 32-key tile is 128
+// units, moved by two of the four waves.
+constexpr bool prefill_shape(bool fp8, int d, int bs) {
+  const int x = fp8 ? 16 : 8;
+  const bool dim = d == 64 || d == 96 || d == 128 || d == 192 || d == 256;
+  const bool blk = fp8 ? (bs == 16 || bs == 32) : (bs == 8 || bs == 16 || bs == 32);
+  return dim && blk && (d * bs / x) % 64 == 0;
+}
+
+template <typename T, typename C, int D, int BS>
+hipError_t dispatch_if(int group, const PrefillArgs& a, const CacheGeom& g, hipStream_t stream,
+                       bool& done) {
+  constexpr bool kF8 = std::is_same_v<C, fp8_t>;
+  if constexpr (prefill_shape(kF8, D, BS)) {
+    if (g.head_dim == D && g.block_size == BS) {
+      done = true;
+      return dispatch_group<T, C, D, BS>(group, a, g, stream);
+    }
+  }
+  return hipSuccess;
+}
+
+template <typename T, typename C, int D>
+hipError_t dispatch_dim(int group, const PrefillArgs& a, const CacheGeom& g, hipStream_t stream,
+                        bool& done) {
+  hipError_t e = dispatch_if<T, C, D, 8>(group, a, g, stream, done);
+  if (!done) e = dispatch_if<T, C, D, 16>(group, a, g, stream, done);
+  if (!done) e = dispatch_if<T, C, D, 32>(group, a, g, stream, done);
+  return e;
+}
+
 template <typename T, typename C>
 hipError_t dispatch_shape(int group, const PrefillArgs& a, const CacheGeom& g,
                           hipStream_t stream) {
-  constexpr bool kF8 = std::is_same_v<C, fp8_t>;
-  if (g.head_dim == 128) {
-    if (g.block_size == 16) return dispatch_group<T, C, 128, 16>(group, a, g, stream);
-    if (g.block_size == 32) return dispatch_group<T, C, 128, 32>(group, a, g, stream);
-    if constexpr (!kF8)
-      if (g.block_size == 8) return dispatch_group<T, C, 128, 8>(group, a, g, stream);
-  }
-  if (g.head_dim == 64) {
-    if constexpr (!kF8)
-      if (g.block_size == 8) return dispatch_group<T, C, 64, 8>(group, a, g, stream);
-    if (g.block_size == 16) return dispatch_group<T, C, 64, 16>(group, a, g, stream);
-    if (g.block_size == 32) return dispatch_group<T, C, 64, 32>(group, a, g, stream);
-  }
-  return hipErrorInvalidValue;
+  bool done = false;
+  hipError_t e = dispatch_dim<T, C, 128>(group, a, g, stream, done);
+  if (!done) e = dispatch_dim<T, C, 64>(group, a, g, stream, done);
+  if (!done) e = dispatch_dim<T, C, 96>(group, a, g, stream, done);
+  if (!done) e = dispatch_dim<T, C, 192>(group, a, g, stream, done);
+  if (!done) e = dispatch_dim<T, C, 256>(group, a, g, stream, done);
+  return done ? e : hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -754,10 +798,9 @@ bool prefill_supported(int dtype, int cache_dtype, int head_dim, int block_size,
   if (!(dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) || !(group == 1 || group == 2 ||
                                                                 group == 4))
     return false;
-  if (cache_dtype == VPA_DTYPE_FP8_E4M3)
-    return (head_dim == 64 || head_dim == 128) && (block_size == 16 || block_size == 32);
-  return cache_dtype == dtype && (head_dim == 64 || head_dim == 128) &&
-         (block_size == 8 || block_size == 16 || block_size == 32);
+  const bool fp8 = cache_dtype == VPA_DTYPE_FP8_E4M3;
+  if (!fp8 && cache_dtype != dtype) return false;
+  return prefill_shape(fp8, head_dim, block_size);
 }
 
 int prefill_positions_per_workgroup(int group) { return kPrefillWaves * 32 / group; }

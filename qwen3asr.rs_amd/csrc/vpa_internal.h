@@ -177,6 +177,9 @@ hipError_t launch_paged_read(int cache_dtype, const void* key_cache, const void*
 // True when a decode kernel is compiled for this (dtype, head_dim, block_size,
 // query heads per kv head) combination.
 bool decode_supported(int dtype, int head_dim, int block_size, int group);
+// 16-bit caches at head_dim 64 and 128 decode with the rows kernel (and its
+// work list); every other shape with the generic split-K kernel.
+bool decode_uses_rows_kernel(int dtype, int head_dim);
 bool cache_kernels_supported(int dtype, int head_dim, int block_size);
 
 }  // namespace vpa

@@ -85,7 +85,7 @@ def rc_call(**over):
 @pytest.mark.parametrize("over,code,needle", [
     (dict(dtype=_lib.DTYPE_F32), _lib.VPA_ERR_UNSUPPORTED, "differs"),
     (dict(dtype=7, cdtype=7), _lib.VPA_ERR_UNSUPPORTED, "dtype"),
-    (dict(d=96), _lib.VPA_ERR_UNSUPPORTED, "no kernel"),
+    (dict(d=80), _lib.VPA_ERR_UNSUPPORTED, "no kernel"),
     (dict(bs=24), _lib.VPA_ERR_UNSUPPORTED, "no kernel"),
     (dict(hstride=100), _lib.VPA_ERR_INVALID_ARGUMENT, "strides"),
     (dict(bstride=128 * 16), _lib.VPA_ERR_INVALID_ARGUMENT, "strides"),
@@ -187,8 +187,12 @@ def pf_call(**over):
 @pytest.mark.parametrize("over,code,needle", [
     (dict(dtype=_lib.DTYPE_F32, cdtype=_lib.DTYPE_F32, bstride=8 * 128 * 16 * 2,
           hstride=128 * 16 * 2), _lib.VPA_ERR_UNSUPPORTED, "no MFMA kernel"),
-    (dict(d=256, bstride=8 * 256 * 16, hstride=256 * 16), _lib.VPA_ERR_UNSUPPORTED,
+    (dict(d=96, bs=8, bstride=8 * 96 * 8, hstride=96 * 8), _lib.VPA_ERR_UNSUPPORTED,
      "no MFMA kernel"),
+    (dict(d=80, bstride=8 * 80 * 16, hstride=80 * 16), _lib.VPA_ERR_UNSUPPORTED,
+     "no kernel for dtype"),
+    (dict(cdtype=_lib.DTYPE_FP8_E4M3, ks=FAKE, vs=FAKE, d=96, bs=16, bstride=8 * 96 * 16,
+          hstride=96 * 16), _lib.VPA_ERR_UNSUPPORTED, "no MFMA kernel"),
     (dict(h=64), _lib.VPA_ERR_UNSUPPORTED, "no MFMA kernel"),
     (dict(h=12), _lib.VPA_ERR_INVALID_ARGUMENT, "multiple"),
     (dict(cdtype=_lib.DTYPE_F16), _lib.VPA_ERR_UNSUPPORTED, "differs"),
@@ -204,6 +208,37 @@ def test_prefill_host_validation(over, code, needle):
     rc, msg = pf_call(**over)
     assert rc == code, msg
     assert needle in msg
+
+
+@pytest.mark.parametrize("d,bs,fp8", [(96, 16, False), (96, 32, False), (192, 8, False),
+                                      (256, 8, False), (256, 32, False), (96, 32, True),
+                                      (192, 16, True), (256, 32, True)])
+def test_prefill_head_dims_pass_validation(d, bs, fp8):
+    """head_dim 96 / 192 / 256 (the Metal prefill's set, varlen_prefill.rs:15)
+    pass every host check; an empty batch then returns before any launch."""
+    x = 16 if fp8 else 8
+    over = dict(d=d, bs=bs, bstride=8 * d * bs, hstride=d * bs, maxq=0)
+    if fp8:
+        over.update(cdtype=FP8, ks=FAKE, vs=FAKE)
+    assert (d * bs // x) % 64 == 0
+    rc, msg = pf_call(**over)
+    assert rc == 0, msg
+
+
+@pytest.mark.parametrize("d,bs,dtype,ok", [
+    (96, 8, _lib.DTYPE_BF16, False), (96, 16, _lib.DTYPE_BF16, True),
+    (96, 8, _lib.DTYPE_F32, True), (192, 8, _lib.DTYPE_F16, True),
+    (80, 16, _lib.DTYPE_BF16, False)])
+def test_decode_head_dims_validation(d, bs, dtype, ok):
+    """Decode at head_dim 96 and 192: a (block, head) tile must be whole 1 KiB
+    wave loads (16-bit head_dim 96 needs 16- or 32-token blocks)."""
+    rc, msg = pa_call(d=d, bs=bs, dtype=dtype, cdtype=dtype, bstride=8 * d * bs,
+                      hstride=d * bs, b=0)
+    if ok:
+        assert rc == 0, msg
+    else:
+        assert rc == _lib.VPA_ERR_UNSUPPORTED, msg
+        assert "head_dim" in msg
 
 
 def test_prefill_empty_is_noop():

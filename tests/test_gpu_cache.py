@@ -30,7 +30,7 @@ def run_append(device, code, kvh, d, bs, nb, slots, seed, zero_cache=False):
 
 @pytest.mark.parametrize("code", [orc.F32, orc.BF16, orc.F16])
 @pytest.mark.parametrize("bs", [8, 16, 32])
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [64, 96, 128, 192, 256])
 def test_append_decode_pattern(device, code, bs, d):
     """One token per sequence into scattered blocks (the decode append)."""
     rng = np.random.default_rng(bs * d + code)
@@ -152,6 +152,26 @@ def test_gather_kv_cache(device, code, bs):
     kc, vc = make_cache(rng, nb, kvh, d, bs, code)
     bt = block_tables_for(rng, lens, nb, bs, pad_cols=2)
     bt[1, 1] = nb + 3       # beyond the sequence: never read
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    gk, gv = vpa.gather_kv_cache(to_dev(kc, code, device), to_dev(vc, code, device), None, None,
+                                 u32(bt, device), u32(cu, device), TORCH[code])
+    torch.cuda.synchronize()
+    ek, ev = orc.gather_kv_cache(kc, vc, bt, cu, dtype=code)
+    np.testing.assert_array_equal(to_host(gk), ek)
+    np.testing.assert_array_equal(to_host(gv), ev)
+
+
+@pytest.mark.parametrize("code", [orc.F32, orc.BF16])
+@pytest.mark.parametrize("bs", [8, 32])
+@pytest.mark.parametrize("d", [96, 192])
+def test_gather_kv_cache_head_dims(device, code, bs, d):
+    """The head dims of the Metal prefill's set (varlen_prefill.rs:15) that
+    are not powers of two."""
+    rng = np.random.default_rng(90 + bs + d + code)
+    nb, kvh = 48, 4
+    lens = [1, bs + 3, 4 * bs - 1, 50]
+    kc, vc = make_cache(rng, nb, kvh, d, bs, code)
+    bt = block_tables_for(rng, lens, nb, bs, pad_cols=1)
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
     gk, gv = vpa.gather_kv_cache(to_dev(kc, code, device), to_dev(vc, code, device), None, None,
                                  u32(bt, device), u32(cu, device), TORCH[code])

@@ -46,13 +46,25 @@ def test_decode_qwen3_asr_shape(device, code, bs):
     assert_attention_close(got, want, code, f"code={code} bs={bs}")
 
 
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [64, 96, 128, 192, 256])
 @pytest.mark.parametrize("h,kvh", [(8, 8), (16, 8), (16, 4)])
 @pytest.mark.parametrize("code", [orc.BF16, orc.F32])
 def test_decode_head_dims_and_groups(device, d, h, kvh, code):
     lens = [3, 64, 300, 777]
     got, want = decode_case(device, code, h, kvh, d, 16, lens, seed=d + h + kvh)
     assert_attention_close(got, want, code, f"d={d} h={h} kvh={kvh}")
+
+
+@pytest.mark.parametrize("d,bs,code", [(96, 32, orc.BF16), (96, 8, orc.F32), (96, 16, orc.F16),
+                                       (192, 8, orc.F16), (192, 32, orc.BF16),
+                                       (192, 16, orc.F32)])
+def test_decode_head_dims_96_192_block_sizes(device, d, bs, code):
+    """head_dim 96 and 192 over the block sizes each cache type takes
+    (16-bit head_dim 96 needs 16- or 32-token blocks), lengths across the
+    256-token partitions of the split-K kernel."""
+    lens = [1, 2, bs - 1, bs + 1, 255, 256, 257, 1300]
+    got, want = decode_case(device, code, 16, 8, d, bs, lens, seed=d + bs + code)
+    assert_attention_close(got, want, code, f"d={d} bs={bs} code={code}")
 
 
 def test_decode_config_c1(device):

@@ -309,6 +309,51 @@ def test_fp8_prefill_head_dim_64(device, bs, causal):
     assert_attention_close(got, want, orc.BF16, f"fp8 prefill d=64 bs={bs} causal={causal}")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("d,bs", [(96, 32), (192, 16), (192, 32), (256, 16), (256, 32)])
+def test_fp8_prefill_head_dims(device, d, bs, causal):
+    """The Metal prefill's other head dims (varlen_prefill.rs:15) over fp8
+    caches (head_dim 96 needs 32-token blocks at fp8)."""
+    got, want, _ = fp8_prefill_case(device, orc.BF16, 16, 8, bs, PF_PRIOR, PF_NEW,
+                                    seed=d + bs + causal, causal=causal, d=d,
+                                    scales=(0.37, 3.1))
+    assert np.isfinite(got).all()
+    assert_attention_close(got, want, orc.BF16, f"fp8 prefill d={d} bs={bs} causal={causal}")
+
+
+@pytest.mark.parametrize("d", [96, 192])
+def test_fp8_append_and_gather_head_dims(device, d):
+    """Append into and gather out of fp8 caches at head_dim 96 and 192:
+    bit-exact bytes and dequantised rows."""
+    rng = np.random.default_rng(d)
+    kvh, bs, nb = 4, 32, 16
+    lens = np.array([5, 40, 70], dtype=np.uint32)
+    bt = block_tables_for(rng, lens, nb, bs)
+    pos = [np.arange(int(L)) for L in lens]
+    slots = np.concatenate([bt[s, p // bs].astype(np.int64) * bs + p % bs
+                            for s, p in enumerate(pos)])
+    t = len(slots)
+    k = orc.from_f32(spread_values(rng, (t, kvh, d)), orc.BF16)
+    v = orc.from_f32(spread_values(rng, (t, kvh, d)), orc.BF16)
+    kc = np.zeros((nb, kvh, d // 16, bs, 16), np.uint8)
+    vc = np.zeros((nb, kvh, d, bs), np.uint8)
+    kcd, vcd = f8(kc, device), f8(vc, device)
+    vpa.reshape_and_cache(to_dev(k, orc.BF16, device), to_dev(v, orc.BF16, device),
+                          scalar(0.5, device), scalar(2.0, device), kcd, vcd, i64(slots, device))
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    gk, gv = vpa.gather_kv_cache(kcd, vcd, scalar(0.5, device), scalar(2.0, device),
+                                 u32(bt, device), u32(cu, device), TORCH[orc.F32])
+    torch.cuda.synchronize()
+    orc.reshape_and_cache_fp8(k, v, kc, vc, slots, orc.BF16, 0.5, 2.0)
+    np.testing.assert_array_equal(f8_host(kcd), kc)
+    np.testing.assert_array_equal(f8_host(vcd), vc)
+    wk, wv = orc.gather_kv_cache_fp8(kc, vc, bt, cu, orc.F32, 0.5, 2.0)
+    for got, want in ((to_host(gk), wk), (to_host(gv), wv)):
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        fin = ~np.isnan(want)
+        np.testing.assert_array_equal(got[fin], want[fin])
+
+
 @pytest.mark.parametrize("d", [64, 128])
 def test_fp8_prefill_equals_bf16_prefill_over_dequantised_cache(device, d):
     """Scales 1: E4M3 values are exact in bf16, so the fp8 kernel feeds the

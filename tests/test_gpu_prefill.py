@@ -71,12 +71,25 @@ def test_prefill_qwen3_asr_shape(device, code, bs, causal):
     assert_attention_close(got, want, code, f"code={code} bs={bs} causal={causal}")
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 96, 128, 192, 256])
 @pytest.mark.parametrize("h,kvh", [(8, 8), (16, 8), (16, 4)])
 def test_prefill_head_dims_and_groups(device, d, h, kvh):
     got, want = prefill_case(device, orc.BF16, h, kvh, d, 16, [7, 0, 260], [40, 65, 17],
                              seed=d + h + kvh)
     assert_attention_close(got, want, orc.BF16, f"d={d} h={h} kvh={kvh}")
+
+
+@pytest.mark.parametrize("d,bs,code,causal", [
+    (96, 32, orc.F16, True), (96, 16, orc.BF16, False), (192, 8, orc.BF16, False),
+    (192, 32, orc.F16, True), (256, 8, orc.BF16, True), (256, 32, orc.BF16, False),
+    (256, 16, orc.F16, True)])
+def test_prefill_head_dims_block_sizes(device, d, bs, code, causal):
+    """The Metal prefill's head dims (varlen_prefill.rs:15) over the block
+    sizes: ragged prior and new lengths, stale NaN in every unused slot."""
+    got, want = prefill_case(device, code, 16, 8, d, bs, RAGGED_PRIOR, RAGGED_NEW,
+                             seed=d + bs + code + causal, causal=causal, stale_nan=True)
+    assert np.isfinite(got).all()
+    assert_attention_close(got, want, code, f"d={d} bs={bs} code={code} causal={causal}")
 
 
 @pytest.mark.parametrize("scale", [-0.125, 1.0, 4.0])
