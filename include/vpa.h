@@ -79,7 +79,8 @@ const char* vpa_version(void);
  * or 32 (the append and the gather every combination; decode and prefill
  * need a (block, head) tile of a whole number of KiB, head_dim * block_size
  * / x a multiple of 64, so head_dim 96 needs 16- or 32-token blocks at 16
- * bits and 32-token blocks at fp8). Other shapes return VPA_ERR_UNSUPPORTED.
+ * bits and 32-token blocks at fp8, and fp8 at 8-token blocks head_dim 128
+ * or 256). Other shapes return VPA_ERR_UNSUPPORTED.
  */
 int vpa_cache_layout(int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                      int64_t num_blocks, int32_t cache_dtype, int64_t* key_shape,
@@ -148,7 +149,8 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * alibi_slopes and sinks must be NULL and softcapping must be 1.0 (the only
  * values vASR passes); anything else returns VPA_ERR_UNSUPPORTED.
  * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 with a bf16 or f16
- * query (head_dim 64 or 128, block_size 16 or 32): K and V are then read as
+ * query (head_dim 64 or 128 with block_size 16 or 32, head_dim 128 with
+ * block_size 8): K and V are then read as
  * (float)byte * (*k_scale) and (float)byte * (*v_scale), k_scale / v_scale
  * being device pointers to one f32 each (ignored for 16/32-bit caches).
  * workspace must hold vpa_paged_attention_workspace_size(...) bytes (always
@@ -312,8 +314,9 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
  * Head dims 64, 96, 128, 192 and 256 (the Metal kernel's set,
  * varlen_prefill.rs:15), 1, 2 or 4 query heads per kv head.
  * cache_dtype equals dtype (block_size 8, 16 or 32), or is
- * VPA_DTYPE_FP8_E4M3 (block_size 16 or 32) for bf16/f16 queries; head_dim 96
- * needs 16- or 32-token blocks at 16 bits and 32-token blocks at fp8. The
+ * VPA_DTYPE_FP8_E4M3 (block_size 8, 16 or 32) for bf16/f16 queries; head_dim
+ * 96 needs 16- or 32-token blocks at 16 bits and 32-token blocks at fp8, fp8
+ * at 8-token blocks head_dim 128 or 256. The
  * cache is read as byte *
  * k_scale / byte * v_scale (the Metal kernel's fp8 path,
  * prefill_paged_attn.metal:698-769), converted to the query type in

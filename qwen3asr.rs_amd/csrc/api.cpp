@@ -272,10 +272,12 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
   if (rc != VPA_OK) return rc;
   rc = check_scales(op, cache_dtype, k_scale, v_scale);
   if (rc != VPA_OK) return rc;
-  if (fp8 && !((head_dim == 64 || head_dim == 128) && (block_size == 16 || block_size == 32)))
+  if (fp8 && !((head_dim == 64 || head_dim == 128) && (block_size == 16 || block_size == 32)) &&
+      !(fp8 && head_dim == 128 && block_size == 8))
     return fail(VPA_ERR_UNSUPPORTED,
-                "%s: fp8 cache needs head_dim 64 or 128 and block_size 16 or 32 (got %d, %d)", op,
-                head_dim, block_size);
+                "%s: fp8 cache needs head_dim 64 or 128 with block_size 16 or 32, or head_dim 128 "
+                "with block_size 8 (got %d, %d)",
+                op, head_dim, block_size);
   if (num_seqs < 0 || num_heads <= 0 || max_context_len < 0 || block_table_stride < 0)
     return fail(VPA_ERR_INVALID_ARGUMENT,
                 "%s: bad sizes num_seqs=%d num_heads=%d max_context_len=%d "
@@ -566,8 +568,8 @@ int vpa_chunked_prefill_paged_attention(
     return fail(VPA_ERR_UNSUPPORTED,
                 "%s: no MFMA kernel for dtype=%s cache=%s head_dim=%d block_size=%d group=%d "
                 "(bf16/f16, head_dim 64/96/128/192/256, block_size 8/16/32, 1/2/4 query "
-                "heads per kv head; fp8 caches: block_size 16/32; head_dim 96 needs "
-                "16- or 32-token blocks at 16 bits and 32-token blocks at fp8)",
+                "heads per kv head; head_dim 96 needs 16- or 32-token blocks at 16 bits and "
+                "32-token blocks at fp8; fp8 at 8-token blocks: head_dim 128/256)",
                 op, dtype_name(dtype), dtype_name(cache_dtype), head_dim, block_size, group);
   if (num_seqs == 0 || max_query_len == 0 || total_query_rows == 0) return VPA_OK;
   {

@@ -486,8 +486,12 @@ void paged_decode_rows_kernel(
   constexpr int X = pack_x<C>();
   static_assert(X == (kF8 ? 16 : 8), "16-bit or fp8 cache elements only");
   constexpr int PB = PT / BS;        // blocks per wave partition
-  constexpr int VPR = BS / X;        // 16-byte vectors per value row
-  constexpr int NVV = D * VPR / 64;  // value vectors per lane per block
+  // fp8 at 8-token blocks: a 16-byte value vector holds two rows (dims 2r
+  // and 2r + 1) of the block's 8 tokens; otherwise VPR vectors make a row.
+  constexpr bool kPairRows = kF8 && BS == 8;
+  constexpr int VPR = kPairRows ? 1 : BS / X;  // 16-byte vectors per value row
+  constexpr int NVV = D * BS / X / 64;          // value vectors per lane per block
+  constexpr int NACC = kPairRows ? 2 * NVV : NVV;  // value rows per lane
   constexpr int DSTEP = 64 / VPR;    // row stride between a lane's value vectors
   constexpr int NPL = PT / 64;       // partition tokens per lane in the softmax
   // Stages of NV loads per lane: 8 (8 KiB per wave) for 16-bit caches, 4
@@ -552,14 +556,14 @@ void paged_decode_rows_kernel(
   const int b_begin = c_begin + (c_nb * wave) / NW;
   const int nb = c_begin + (c_nb * (wave + 1)) / NW - b_begin;  // 0: idle wave
 
-  float acc[G][NVV];
+  float acc[G][NACC];
   float m[G], lsum[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
     lsum[g] = 0.f;
 #pragma unroll
-    for (int k = 0; k < NVV; ++k) acc[g][k] = 0.f;
+    for (int k = 0; k < NACC; ++k) acc[g][k] = 0.f;
   }
 
   float vs = 1.f;  // value scale of an fp8 cache
@@ -655,6 +659,37 @@ void paged_decode_rows_kernel(
         uint4 vv[NVV];
 #pragma unroll
         for (int k = 0; k < NVV; ++k) vv[k] = buf[u * KPL + k];
+        if constexpr (kPairRows) {
+          // vector k of lane l: rows 2 (l + 64 k) and 2 (l + 64 k) + 1, the
+          // block's 8 tokens each, against the block's 8 probabilities
+          const int tok0 = (b_begin + bi) * BS;
+#pragma unroll
+          for (int k = 0; k < NVV; ++k) {
+            uint4 vh[2];
+            fp8x16_to_pk<T>(vv[k], vh[0], vh[1]);
+            if (tok0 + BS > L) {  // past the context in the last block: stale values
+#pragma unroll
+              for (int h2 = 0; h2 < 2; ++h2) {
+                union {
+                  uint4 v;
+                  uint16_t e[8];
+                } wv;
+                wv.v = vh[h2];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  if (tok0 + e >= L) wv.e[e] = 0;
+                vh[h2] = wv.v;
+              }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const uint4 pk = *reinterpret_cast<const uint4*>(&my_p[g * PT + bi * BS]);
+              acc[g][2 * k] = dot16<T>(pk, vh[0], acc[g][2 * k]);
+              acc[g][2 * k + 1] = dot16<T>(pk, vh[1], acc[g][2 * k + 1]);
+            }
+          }
+          continue;
+        }
         const int tok0 = (b_begin + bi) * BS + seg * X;
         if constexpr (kF8) {
 #pragma unroll
@@ -767,7 +802,7 @@ void paged_decode_rows_kernel(
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int k = 0; k < NVV; ++k) {
+      for (int k = 0; k < NACC; ++k) {
         if constexpr (VPR >= 2) acc[g][k] += dpp<kDppQuadXor1>(acc[g][k]);
         if constexpr (VPR >= 4) acc[g][k] += dpp<kDppQuadXor2>(acc[g][k]);
         if constexpr (kF8) acc[g][k] *= vs;
@@ -780,12 +815,19 @@ void paged_decode_rows_kernel(
   __syncthreads();
   {
     float* my_row = &s_logit[wave][0][0];
-    const int row0 = lane / VPR;
-    if (lane % VPR == 0) {
+    if constexpr (kPairRows) {
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int k = 0; k < NVV; ++k) my_row[g * D + row0 + k * DSTEP] = acc[g][k];
+        for (int k = 0; k < NACC; ++k) my_row[g * D + 2 * (lane + 64 * (k / 2)) + k % 2] = acc[g][k];
+    } else {
+      const int row0 = lane / VPR;
+      if (lane % VPR == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int k = 0; k < NVV; ++k) my_row[g * D + row0 + k * DSTEP] = acc[g][k];
+      }
     }
     if (lane == 0) {
 #pragma unroll
@@ -1092,7 +1134,8 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (D == 64 && BS == 16) { VPA_DECODE_FP8_G(T, 64, 16) }     \
   if (D == 64 && BS == 32) { VPA_DECODE_FP8_G(T, 64, 32) }     \
   if (D == 128 && BS == 16) { VPA_DECODE_FP8_G(T, 128, 16) }   \
-  if (D == 128 && BS == 32) { VPA_DECODE_FP8_G(T, 128, 32) }
+  if (D == 128 && BS == 32) { VPA_DECODE_FP8_G(T, 128, 32) }   \
+  if (D == 128 && BS == 8) { VPA_DECODE_FP8_G(T, 128, 8) }
 
 // fp8 caches: the rows kernel for bf16 / f16 queries.
 template <typename... A>

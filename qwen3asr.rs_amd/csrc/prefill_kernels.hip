@@ -275,7 +275,11 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   constexpr int PPB = kPrefillWaves * PPW;  // query positions per workgroup
   constexpr int KS = D / 16;    // k-steps of Q.K^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
-  constexpr int UB = BS / X;    // 16-byte units per value row of a block
+  // fp8 at 8-token blocks: a 16-byte value unit holds two dims (2r, 2r + 1)
+  // of the block's 8 keys and is copied to LDS as it is; otherwise the
+  // units of a block's value rows are transposed to [key unit][dim]
+  constexpr bool kPairRows = kF8 && BS == 8;
+  constexpr int UB = kPairRows ? 1 : BS / X;  // 16-byte units per value row of a block
   constexpr int NU = D * KT / X;                   // 16-byte units per K (and per V) tile
   constexpr int NDMA = NU / 64;                    // DMAs per K (and per V) tile
   // DMAs per issuing wave per K (and per V) tile; the first DMW waves issue
@@ -283,7 +287,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   constexpr int DMW = NDMA / DPW;
   constexpr int DPT = 2 * DPW;                     // DMAs per wave per tile
   constexpr int NBT = KT / BS;                     // blocks per tile
-  constexpr int RBV = D * UB;                      // units of one block's K (or V) rows
+  constexpr int RBV = D * BS / X;                  // units of one block's K (or V) rows
   constexpr int DPB = RBV / 64;                    // DMAs per block region
   // LDS units between the K regions of two blocks: with 8-key blocks, the 16
   // lanes of one LDS read pass span two blocks, padded to other banks
@@ -405,7 +409,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   for (int i = 0; i < DPW; ++i) {
     const int r = ((wave * DPW + i) % DPB) * 64 + lane;  // unit of the block region
     koff[i] = (uint32_t)(r * X);
-    voff[i] = (uint32_t)((r % D) * BS + (r / D) * X);
+    voff[i] = kPairRows ? (uint32_t)(r * X) : (uint32_t)((r % D) * BS + (r / D) * X);
   }
 
   // Issue the DMAs of the SUB tiles of step t into stage S (always all SUB
@@ -458,11 +462,16 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   // (g / UB) * RBV + (g % UB) * D units; that splits into a k2 and a half term
   // (fp8: units hold 16 keys; keys 8g .. 8g+7 are bytes 8 (g % 2) .. of
   // unit g / 2)
+  // (fp8 at 8-token blocks: keys 8g .. 8g+7 of dim d are bytes 8 (d % 2) ..
+  // of unit d / 2 of block region g)
   auto vgroup = [](int g) { return (g / UB) * RBV + (g % UB) * D; };
-  constexpr int kVStep1 = kF8 ? ((1 / UB) * RBV + (1 % UB) * D) * 16
-                              : ((2 / UB) * RBV + (2 % UB) * D) * 16;
-  const uint32_t va_lane =
-      kF8 ? (uint32_t)(col * 16 + 8 * half) : (uint32_t)((vgroup(half) + col) * 16);
+  constexpr int kVStep1 = kPairRows ? 2 * RBV * 16
+                          : kF8     ? ((1 / UB) * RBV + (1 % UB) * D) * 16
+                                    : ((2 / UB) * RBV + (2 % UB) * D) * 16;
+  constexpr int kVStepD = kPairRows ? 32 * 8 : 32 * 16;  // LDS bytes between 32-dim tiles
+  const uint32_t va_lane = kPairRows ? (uint32_t)(half * RBV * 16 + col * 8)
+                           : kF8     ? (uint32_t)(col * 16 + 8 * half)
+                                     : (uint32_t)((vgroup(half) + col) * 16);
 
   // keys of tile t that exist: inside the context and in a present block
   // (uniform over the workgroup)
@@ -487,7 +496,10 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
     const uint32_t absent = ~vmask;
     for (int e = tid; e < KT * D; e += kPrefillThreads) {
       const int k = e / D, d = e % D;
-      if ((absent >> k) & 1u) ve[(vgroup(k / X) + d) * X + k % X] = 0;
+      if ((absent >> k) & 1u) {
+        if constexpr (kPairRows) ve[(k / BS) * RBV * 16 + d * 8 + k % BS] = 0;
+        else ve[(vgroup(k / X) + d) * X + k % X] = 0;
+      }
     }
   };
 
@@ -546,7 +558,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
     v4i_t vop[DT][2];
     if constexpr (kF8) {
       v2i_t v8[DT][2];
-      lds_read_pairs8<32 * 16, kVStep1>(v8, va_lane + lds_addr(sv),
+      lds_read_pairs8<kVStepD, kVStep1>(v8, va_lane + lds_addr(sv),
                                         std::make_integer_sequence<int, DT>{});
       lgkm_wait(v8);
 #pragma unroll
@@ -746,15 +758,15 @@ hipError_t dispatch_group(int group, const PrefillArgs& a, const CacheGeom& g,
   }
 }
 
-// Shapes: head_dim 64, 96, 128, 192 or 256 with a (block, head) tile of a
-// whole number of 1 KiB DMAs (D * BS / x a multiple of 64 units): 16-bit
-// caches at block sizes 8, 16, 32 (head_dim 96 at 16 and 32); fp8 caches at
-// 16 and 32 (head_dim 96 at 32). At fp8 head_dim 64 a 32-key tile is 128
-// units, moved by two of the four waves.
+// Shapes: head_dim 64, 96, 128, 192 or 256, block sizes 8, 16, 32, with a
+// (block, head) tile of a whole number of 1 KiB DMAs (D * BS / x a multiple
+// of 64 units): head_dim 96 at 16-bit needs 16- or 32-token blocks, at fp8
+// 32-token ones; fp8 at 8-token blocks takes head_dim 128 and 256. At fp8
+// head_dim 64 a 32-key tile is 128 units, moved by two of the four waves.
 constexpr bool prefill_shape(bool fp8, int d, int bs) {
   const int x = fp8 ? 16 : 8;
   const bool dim = d == 64 || d == 96 || d == 128 || d == 192 || d == 256;
-  const bool blk = fp8 ? (bs == 16 || bs == 32) : (bs == 8 || bs == 16 || bs == 32);
+  const bool blk = bs == 8 || bs == 16 || bs == 32;
   return dim && blk && (d * bs / x) % 64 == 0;
 }
 

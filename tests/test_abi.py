@@ -328,8 +328,8 @@ def test_reshape_and_cache_fp8_accepts_every_float_input(dtype):
     (dict(cdtype=FP8, **F8_STRIDES), _lib.VPA_ERR_INVALID_ARGUMENT, "k_scale and v_scale"),
     (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES),
      _lib.VPA_ERR_UNSUPPORTED, "differs"),
-    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bstride=8 * 128 * 8, hstride=128 * 8),
-     _lib.VPA_ERR_UNSUPPORTED, "block_size 16 or 32"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bs=8, bstride=8 * 64 * 8, hstride=64 * 8),
+     _lib.VPA_ERR_UNSUPPORTED, "block_size 8"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bstride=8 * 256 * 16, hstride=256 * 16),
      _lib.VPA_ERR_UNSUPPORTED, "head_dim 64 or 128"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES), _lib.VPA_ERR_WORKSPACE, "workspace"),
@@ -355,8 +355,19 @@ def test_gather_and_prefill_fp8_validation():
     assert rc == _lib.VPA_ERR_INVALID_ARGUMENT and "k_scale" in msg, msg
     rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, dtype=_lib.DTYPE_F32, **F8_STRIDES)
     assert rc == _lib.VPA_ERR_UNSUPPORTED and "differs" in msg, msg
-    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bstride=8 * 128 * 8, hstride=128 * 8)
+    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bs=8, bstride=8 * 64 * 8,
+                      hstride=64 * 8)
     assert rc == _lib.VPA_ERR_UNSUPPORTED and "no MFMA kernel" in msg, msg
+    # fp8 at 8-token blocks: head_dim 128 (decode and prefill) and 256 (prefill)
+    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bstride=8 * 128 * 8, hstride=128 * 8,
+                      maxq=0)
+    assert rc == 0, msg
+    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bs=8, bstride=8 * 256 * 8,
+                      hstride=256 * 8, maxq=0)
+    assert rc == 0, msg
+    rc, msg = pa_call(cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bstride=8 * 128 * 8, hstride=128 * 8,
+                      b=0)
+    assert rc == 0, msg
 
 
 def test_paged_cache_read_validation():

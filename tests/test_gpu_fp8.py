@@ -173,6 +173,19 @@ def test_fp8_decode_head_dims_and_groups(device, d, h, kvh):
     assert_attention_close(got, want, orc.BF16, f"fp8 d={d} h={h} kvh={kvh}")
 
 
+@pytest.mark.parametrize("planned", [False, True])
+@pytest.mark.parametrize("h,kvh", [(16, 8), (16, 4)])
+def test_fp8_decode_block_size_8(device, h, kvh, planned):
+    """8-token blocks (paged_cache_runtime.rs:406-411 allows 8, 16, 32 for
+    any cache type): a 16-byte value vector then holds two dims of the
+    block's 8 tokens. Lengths across wave and chunk boundaries, stale NaN
+    bytes past each context."""
+    lens = [1, 7, 8, 9, 511, 512, 513, 2047, 2049, 3000]
+    got, want = fp8_decode_case(device, orc.BF16, h, kvh, 128, 8, lens, seed=h + kvh + planned,
+                                scales=(0.37, 3.1), planned=planned)
+    assert_attention_close(got, want, orc.BF16, f"fp8 bs=8 h={h} kvh={kvh}")
+
+
 @pytest.mark.parametrize("scales", [(0.37, 3.1), (4.0, 0.25)])
 def test_fp8_decode_scales_and_planned(device, scales):
     lens = [5, 700, 1100, 2049]
@@ -319,6 +332,43 @@ def test_fp8_prefill_head_dims(device, d, bs, causal):
                                     scales=(0.37, 3.1))
     assert np.isfinite(got).all()
     assert_attention_close(got, want, orc.BF16, f"fp8 prefill d={d} bs={bs} causal={causal}")
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("d", [128, 256])
+def test_fp8_prefill_block_size_8(device, d, causal, code):
+    """fp8 caches at 8-token blocks: each value unit holds two dims of a
+    block's keys, copied to LDS as is; absent blocks and NaN bytes in every
+    unused slot."""
+    def mutate(bt):
+        bt[3, 2] = 1 << 30  # an absent block inside sequence 3's context
+    got, want, _ = fp8_prefill_case(device, code, 16, 8, 8, PF_PRIOR, PF_NEW,
+                                    seed=d + causal + code, causal=causal, d=d,
+                                    scales=(0.37, 3.1), mutate_bt=mutate)
+    assert np.isfinite(got).all()
+    assert_attention_close(got, want, code, f"fp8 prefill bs=8 d={d} causal={causal}")
+
+
+def test_fp8_prefill_block_size_8_equals_bf16_over_dequantised_cache(device):
+    """Scales 1 at 8-token blocks: bit-equal to the bf16 kernel over a bf16
+    copy of the cache (the two-dims-per-unit value layout feeds the MFMAs
+    the same operands)."""
+    code, h, kvh, bs = orc.BF16, 16, 8, 8
+    got, _, (q, kc, vc, bt, lens, cu, scale) = fp8_prefill_case(
+        device, code, h, kvh, bs, [0, 17, 500], [64, 33, 90], seed=23, d=128)
+    nb, _, c16, _, _ = kc.shape
+    d = c16 * 16
+    kf = orc.fp8_to_f32(kc).transpose(0, 1, 3, 2, 4).reshape(nb, kvh, bs, d)
+    kb = orc.from_f32(np.ascontiguousarray(
+        kf.reshape(nb, kvh, bs, d // 8, 8).transpose(0, 1, 3, 2, 4)), code)
+    vb = orc.from_f32(orc.fp8_to_f32(vc), code)
+    ref = vpa.paged_attention_varlen_prefill(
+        to_dev(q, code, device), to_dev(kb, code, device), to_dev(vb, code, device),
+        u32(bt, device), u32(lens, device), u32(cu, device), None, None, scale, 1.0,
+        causal=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.view(np.uint32), orc.to_f32(to_host(ref), code).view(np.uint32))
 
 
 @pytest.mark.parametrize("d", [96, 192])
