@@ -33,10 +33,11 @@
 // with its operand conversions, needs most; both cache types use the same
 // steps, so their rescale points, and with scales 1 their results, agree).
 // K and V tiles travel HBM -> LDS by the LDS-DMA form of the 16-byte global
-// load (no VGPR round trip) into kPrefillStages stage buffers; step
-// t + stages - 1 is issued while step t is consumed, waits are explicit
-// vmcnt counts plus a bare workgroup barrier (the compiler's __syncthreads
-// would drain every outstanding DMA), and the operand reads from LDS are
+// load (no VGPR round trip) into two stage buffers; step t + 1 is issued
+// while step t is consumed, waits are explicit vmcnt counts plus a bare
+// workgroup barrier (the compiler's __syncthreads would drain every
+// outstanding DMA), the block ids of a step are loaded two steps before
+// its tiles are consumed, and the operand reads from LDS are
 // written as ds_read with their own lgkmcnt wait so the
 // compiler does not add a full vmcnt drain before them. Each DMA copies 64
 // units of one cache block, so its address is a scalar block base plus a
@@ -87,9 +88,6 @@ __device__ __forceinline__ float max_xor32(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-#ifndef VPA_PREFILL_STAGES
-#define VPA_PREFILL_STAGES 2
-#endif
 #ifndef VPA_PREFILL_WAVES_PER_EU
 #define VPA_PREFILL_WAVES_PER_EU 2
 #endif
@@ -98,14 +96,12 @@ __device__ __forceinline__ float max_xor32(float v) {
 #endif
 constexpr int kPrefillKeys = 32;                    // keys per tile
 constexpr int kPrefillSub = VPA_PREFILL_SUB;        // tiles per pipeline step
-constexpr int kPrefillStages = VPA_PREFILL_STAGES;  // LDS step buffers (steps in flight + 1)
 static_assert(kPrefillSub == 1 || kPrefillSub == 2, "tiles per step");
 #ifndef VPA_PREFILL_WAVES
 #define VPA_PREFILL_WAVES 4
 #endif
 constexpr int kPrefillWaves = VPA_PREFILL_WAVES;  // waves per workgroup, 32 query rows each
 constexpr int kPrefillThreads = 64 * kPrefillWaves;
-static_assert(kPrefillStages >= 2 && kPrefillStages <= 4, "stages");
 
 // s_waitcnt vmcnt(N), leaving the other counters alone (gfx9 encoding).
 template <int N>
@@ -268,7 +264,6 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   constexpr bool kF8 = std::is_same_v<C, fp8_t>;
   static_assert(kF8 || std::is_same_v<C, T>, "cache type is the query type or fp8");
   constexpr int KT = kPrefillKeys;
-  constexpr int NS = kPrefillStages;
   constexpr int SUB = kPrefillSub;
   constexpr int X = kF8 ? 16 : 8;  // cache elements per 16-byte unit
   constexpr int PPW = 32 / G;   // query positions per wave
@@ -285,7 +280,6 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   // DMAs per issuing wave per K (and per V) tile; the first DMW waves issue
   constexpr int DPW = (NDMA + kPrefillWaves - 1) / kPrefillWaves;
   constexpr int DMW = NDMA / DPW;
-  constexpr int DPT = 2 * DPW;                     // DMAs per wave per tile
   constexpr int NBT = KT / BS;                     // blocks per tile
   constexpr int RBV = D * BS / X;                  // units of one block's K (or V) rows
   constexpr int DPB = RBV / 64;                    // DMAs per block region
@@ -302,7 +296,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   // stage buffer: SUB tiles, each K regions [block][chunk][key], then V
   // regions [block][unit][dim]
   constexpr int TU = KU + NU;  // units of one tile in a stage
-  __shared__ __align__(16) uint4 s_t0[SUB * TU], s_t1[SUB * TU], s_t2[SUB * TU], s_t3[SUB * TU];
+  __shared__ __align__(16) uint4 s_t0[SUB * TU], s_t1[SUB * TU];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -388,9 +382,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   auto kst = [&](auto sc, int u) -> uint4* {
     constexpr int S = decltype(sc)::value;
     if constexpr (S == 0) return s_t0 + u * TU;
-    else if constexpr (S == 1) return s_t1 + u * TU;
-    else if constexpr (S == 2) return s_t2 + u * TU;
-    else return s_t3 + u * TU;
+    else return s_t1 + u * TU;
   };
   auto vst = [&](auto sc, int u) -> uint4* { return kst(sc, u) + KU; };
   // block ids of a tile (uniform: scalar loads; the index is clamped to the
@@ -417,9 +409,37 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   // absent blocks read block 0 (in bounds); they are masked in S and their
   // values zeroed when the V operands are built.
   // block ids of the SUB tiles of step t
+  // (with a table row of at least NB entries: one NB-dword scalar load of a
+  // window of the row that holds every entry the step needs, the window
+  // moved back from the sequence's tail so that it stays inside the row;
+  // entries past the last block repeat it, as the per-entry clamp does)
+  constexpr int NB = SUB * NBT;  // block ids of a step
+  const bool wide_ids = block_table_stride >= NB;
   auto step_blocks = [&](int t, uint32_t (&pbs)[SUB][NBT]) {
+    if (!wide_ids) {
 #pragma unroll
-    for (int u = 0; u < SUB; ++u) tile_blocks((t * SUB + u) * KT, pbs[u]);
+      for (int u = 0; u < SUB; ++u) tile_blocks((t * SUB + u) * KT, pbs[u]);
+      return;
+    }
+    const int first = __builtin_amdgcn_readfirstlane(t * SUB * KT / BS);
+    const int base = max(0, min(first, last_blk - (NB - 1)));
+    const uint32_t* p = bt + base;
+    uint32_t w[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) w[i] = p[i];
+    if (first + NB - 1 <= last_blk) {  // base == first
+#pragma unroll
+      for (int i = 0; i < NB; ++i) pbs[i / NBT][i % NBT] = w[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int k = min(first + i, last_blk) - base;
+        uint32_t id = w[0];
+#pragma unroll
+        for (int c = 1; c < NB; ++c) id = k == c ? w[c] : id;
+        pbs[i / NBT][i % NBT] = id;
+      }
+    }
   };
   auto issue = [&](auto sc, int t, const uint32_t (&pbs)[SUB][NBT]) {
     if (DMW < kPrefillWaves && wave >= DMW) return;  // wave issues no DMA (uniform)
@@ -621,25 +641,21 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   };
 
   // one pipeline step: wait for step t's tiles, refill the stage step t-1
-  // used with step t + NS - 1, compute step t
-  auto step = [&](auto sc, int t) {
+  // used with step t + 1, compute step t. The block ids travel ahead of the
+  // steps: pm (step t, for the masks) and pi (step t + 1, for the DMAs
+  // issued here) were loaded two steps and one step earlier, and the ids of
+  // step t + 2 are loaded into pf here, so no step waits for a table load.
+  auto step = [&](auto sc, int t, const uint32_t (&pm)[SUB][NBT],
+                  const uint32_t (&pi)[SUB][NBT], uint32_t (&pf)[SUB][NBT]) {
     if (t >= n_steps) return;
     constexpr int S = decltype(sc)::value;
-    constexpr int DPS = DPT * SUB;  // DMAs per wave per step
-    // block ids of this step (masks) and of the step issued below, loaded
-    // before the waits so that their latency hides behind them
-    const bool refill = t + NS - 1 < n_steps;
-    uint32_t pm[SUB][NBT], pi[SUB][NBT];
-    step_blocks(t, pm);
-    if (refill) step_blocks(t + NS - 1, pi);
-    const int after = min(NS - 2, n_steps - 1 - t);  // later steps already issued
-    if (after >= 2) wait_vmcnt<2 * DPS>();
-    else if (after == 1) wait_vmcnt<DPS>();
-    else wait_vmcnt<0>();
+    const bool refill = t + 1 < n_steps;
+    if (t + 2 < n_steps) step_blocks(t + 2, pf);
+    wait_vmcnt<0>();  // step t's DMAs (the only ones in flight)
     // step t is in LDS for every wave, and every wave is done with step t-1.
     // A bare s_barrier: __syncthreads() would also fence this wave's LDS
-    // writes, i.e. wait for all of its outstanding DMAs, later steps
-    // included; the explicit vmcnt wait above already covers step t.
+    // writes, i.e. wait for all of its outstanding DMAs; the explicit vmcnt
+    // wait above already covers step t.
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -660,26 +676,25 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     }
-    if (refill) issue(Int<(S + NS - 1) % NS>{}, t + NS - 1, pi);
+    if (refill) issue(Int<1 - S>{}, t + 1, pi);
     compute(sc, t, vmask);
   };
   if (n_steps > 0) {
-    uint32_t p0[SUB][NBT];
-    step_blocks(0, p0);
-    issue(Int<0>{}, 0, p0);
-    if (NS > 2 && 1 < n_steps) {
-      step_blocks(1, p0);
-      issue(Int<1 % NS>{}, 1, p0);
-    }
-    if (NS > 3 && 2 < n_steps) {
-      step_blocks(2, p0);
-      issue(Int<2 % NS>{}, 2, p0);
-    }
-    for (int t0 = 0; t0 < n_steps; t0 += NS) {
-      step(Int<0>{}, t0);
-      step(Int<1 % NS>{}, t0 + 1);
-      if constexpr (NS > 2) step(Int<2 % NS>{}, t0 + 2);
-      if constexpr (NS > 3) step(Int<3 % NS>{}, t0 + 3);
+    // ids of steps t0 (a), t0 + 1 (b) and the one loaded two ahead (c)
+    uint32_t ia[SUB][NBT] = {}, ib[SUB][NBT] = {}, ic[SUB][NBT] = {};
+    step_blocks(0, ia);
+    issue(Int<0>{}, 0, ia);
+    if (1 < n_steps) step_blocks(1, ib);
+    for (int t0 = 0; t0 < n_steps; t0 += 2) {
+      step(Int<0>{}, t0, ia, ib, ic);      // loads the ids of t0 + 2 into ic
+      step(Int<1>{}, t0 + 1, ib, ic, ia);  // loads the ids of t0 + 3 into ia
+#pragma unroll
+      for (int u = 0; u < SUB; ++u)
+#pragma unroll
+        for (int i = 0; i < NBT; ++i) {
+          ib[u][i] = ia[u][i];
+          ia[u][i] = ic[u][i];
+        }
     }
   }
 
