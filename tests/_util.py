@@ -60,17 +60,27 @@ def block_tables_for(rng, lens, nb, bs, first=1, pad_cols=0):
     return bt
 
 
+# Floor of the elementwise bound, as a fraction of max|want|. An output near
+# zero is a sum of terms that cancel; its error is the rounding of those
+# terms, not of the result. Measured over the GPU suite (worst element /
+# bound): f32 0.50 and f16 0.375 with a floor of 0.03; bf16 0.72 with 0.1
+# (1.94 with 0.03), and fp8 caches read with bf16 queries up to 1.00 with
+# 0.1: a 5-token context with v_scale 3.1, whose element a CPU emulation of
+# the same arithmetic (probabilities rounded to bf16 for P.V, as the
+# reference's CUDA kernel does) reproduces at the same ratio.
+FLOOR = {orc.F32: 0.03, orc.F16: 0.03, orc.BF16: 0.1}
+
+
 def assert_attention_close(got_f32: np.ndarray, want_f64: np.ndarray, code: int, what=""):
-    """|got - want| <= tol * (|want| + max|want| * 1e-1) per element: relative
-    at the stated tolerance, with a floor of tol/10 of the largest magnitude
-    for entries near zero."""
+    """|got - want| <= tol * (|want| + FLOOR * max|want|) per element: relative
+    at the stated tolerance (TOL), with a floor for entries near zero."""
     tol = TOL[code]
     want = want_f64.astype(np.float64)
     got = got_f32.astype(np.float64)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     scale = np.abs(want).max() if want.size else 0.0
     err = np.abs(got - want)
-    bound = tol * (np.abs(want) + 0.1 * scale) + 1e-30
+    bound = tol * (np.abs(want) + FLOOR[code] * scale) + 1e-30
     worst = np.max(err / bound) if err.size else 0.0
     assert worst <= 1.0, (f"{what}: max err {err.max():.3e} exceeds tol {tol} "
                           f"(ratio {worst:.2f}, max|ref| {scale:.3e})")

@@ -2,15 +2,17 @@
 vasr-paged-attn/src/cuda_graph.rs:204-225): append + paged_attention of
 several layers recorded once, replayed with new per-step metadata copied
 into the captured buffers (cuda_graph.rs:342-371). Every replay is checked
-against the eager ops on the same inputs, with eager work and host
-synchronisation between replays."""
+against the eager ops on the same inputs (bit for bit), with eager work and
+host synchronisation between replays, and every replayed layer's output
+against the fp64 oracle over the caches the replay left."""
 
 import numpy as np
 import pytest
 import torch
 
 import vpa
-from tests._util import block_tables_for
+from oracle import oracle as orc
+from tests._util import assert_attention_close, block_tables_for, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -74,7 +76,12 @@ def test_graph_replay_of_decode_steps_matches_eager(device):
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
+        lens = (lens0 + t).astype(np.uint32)
         for i in range(LAYERS):
             assert torch.equal(out[i], want[i]), f"replay {t} layer {i}"
             assert torch.equal(caches[i][0], saved[i][0]) and torch.equal(caches[i][1],
                                                                            saved[i][1])
+            ref = orc.paged_attention(to_host(q[i]), to_host(caches[i][0]), to_host(caches[i][1]),
+                                      bt_np, lens, max_ctx, D ** -0.5, dtype=orc.BF16)
+            assert_attention_close(orc.to_f32(to_host(out[i]), orc.BF16), ref, orc.BF16,
+                                   f"replay {t} layer {i} vs oracle")

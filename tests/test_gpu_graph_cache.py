@@ -5,15 +5,17 @@ rows: slot 0, context 1, table row 0; columns repeating each row's last).
 A sequence of steps of different batch sizes and table widths (misses,
 hits, and an eviction with a small cache) runs append + paged_attention of
 two layers through the cache; after every step the real rows' outputs
-must equal the eager ops on the unpadded inputs bit for bit, and at the end
-both sets of caches must be equal outside block 0 (the null block the pad
-rows write to)."""
+must equal the eager ops on the unpadded inputs bit for bit and the fp64
+oracle over the caches after the step, and at the end both sets of caches
+must be equal outside block 0 (the null block the pad rows write to)."""
 
 import numpy as np
 import pytest
 import torch
 
 import vpa
+from oracle import oracle as orc
+from tests._util import assert_attention_close, to_host
 from vpa.graph import DecodeGraphCache
 
 pytestmark = pytest.mark.gpu
@@ -107,6 +109,12 @@ def test_graph_cache_padded_replays_equal_eager(device, max_graphs):
         assert cache.captures == captures + (0 if hit else 1), f"step {s}: hit={hit}"
         assert got.shape == want.shape
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"step {s} key {key}"
+        for i, (kc, vc) in enumerate(cg):
+            ref = orc.paged_attention(to_host(rows[f"q{i}"]), to_host(kc), to_host(vc), bt,
+                                      lens.astype(np.uint32), int(lens.max()), D ** -0.5,
+                                      dtype=orc.BF16)
+            assert_attention_close(orc.to_f32(to_host(got[:, i]), orc.BF16), ref, orc.BF16,
+                                   f"step {s} layer {i} vs oracle")
         keys_seen.append(key)
         assert len(cache.graphs) <= max_graphs
     assert any(k == keys_seen[0] for k in keys_seen[1:]), "want a repeated key"
