@@ -311,3 +311,108 @@ def decode_consume_tokens(next_ids, finished, generated, gen_len, eos_ids, eos_f
                                        _ptr(cnt), b)
     return inp, int(cnt[0])
 
+
+
+# ------------------------------------------------------------------ block manager
+class OracleError(RuntimeError):
+    """An error the reference's block manager raises (same message)."""
+
+
+class BlockManager:
+    """Pure-Python restatement of PagedBlockManager
+    (vasr-paged-attn/src/paged_cache_runtime.rs:217-371): a FIFO free list of
+    the block ids 1 .. num_blocks - 1 (block 0 is kept for padded batch rows,
+    :224-231, :271-274), per-request block lists grown by try_allocate_slots
+    (:287-316: take `ceil(tokens / block_size) - held` ids from the front,
+    nothing when the pool has fewer), shrunk by trim_request_to_num_tokens
+    (:322-337) and released by free_request (:350-359), both handing the
+    removed blocks back to the end of the free list last block first."""
+
+    def __init__(self, num_blocks: int, block_size: int):
+        from collections import deque
+
+        self.block_size = int(block_size)
+        self.free = deque(range(1, int(num_blocks)))
+        self.requests: dict[int, list[int]] = {}
+
+    @staticmethod
+    def allocatable_block_capacity(num_blocks: int) -> int:
+        return max(int(num_blocks) - 1, 0)
+
+    def free_blocks(self) -> int:
+        return len(self.free)
+
+    def _needed(self, request_id: int, num_tokens: int) -> int:
+        required = -(-int(num_tokens) // self.block_size)
+        return max(required - len(self.requests.get(request_id, [])), 0)
+
+    def slots_available_for(self, request_id: int, num_tokens: int) -> bool:
+        return self._needed(request_id, num_tokens) <= len(self.free)
+
+    def blocks_for_request(self, request_id: int) -> int:
+        return len(self.requests.get(request_id, []))
+
+    def total_allocated_blocks(self) -> int:
+        return sum(len(b) for b in self.requests.values())
+
+    def try_allocate_slots(self, request_id: int, num_tokens: int) -> bool:
+        needed = self._needed(request_id, num_tokens)
+        if needed == 0:
+            return True
+        if needed > len(self.free):
+            return False
+        ids = self.requests.setdefault(request_id, [])
+        for _ in range(needed):
+            ids.append(self.free.popleft())
+        return True
+
+    def allocate_slots(self, request_id: int, num_tokens: int) -> None:
+        if not self.try_allocate_slots(request_id, num_tokens):
+            raise OracleError(f"paged KV cache exhausted: request_id={request_id} "
+                              f"num_tokens={num_tokens} free_blocks={len(self.free)}")
+
+    def trim_request_to_num_tokens(self, request_id: int, num_tokens: int) -> None:
+        keep = -(-int(num_tokens) // self.block_size)
+        ids = self.requests.get(request_id)
+        if ids is None or keep >= len(ids):
+            return
+        removed = ids[keep:]
+        del ids[keep:]
+        for b in reversed(removed):
+            if b != 0:
+                self.free.append(b)
+
+    def block_ids(self, request_id: int) -> list[int]:
+        if request_id not in self.requests:
+            raise OracleError("paged KV request has no allocated blocks: "
+                              f"request_id={request_id}")
+        return list(self.requests[request_id])
+
+    def free_request(self, request_id: int) -> None:
+        ids = self.requests.pop(request_id, None)
+        if ids is None:
+            return
+        for b in reversed(ids):
+            if b != 0:
+                self.free.append(b)
+
+    def free_many(self, request_ids) -> None:
+        for r in request_ids:
+            self.free_request(r)
+
+    def block_tables_for(self, request_ids) -> list[list[int]]:
+        return [self.block_ids(r) for r in request_ids]
+
+
+def slot_for_position(table, block_size: int, num_blocks: int, position: int) -> int:
+    """slot = table[position / block_size] * block_size + position % block_size
+    (vasr-paged-attn/src/paged_kv_cache.rs:74-103); a position past the
+    table, or a block id past the pool, is the reference's error."""
+    idx = int(position) // int(block_size)
+    if idx >= len(table):
+        raise OracleError(f"missing block table entry: block_idx={idx} position={position}")
+    block = int(table[idx])
+    if block >= int(num_blocks):
+        raise OracleError(f"block id exceeds paged cache capacity: block_id={block} "
+                          f"num_blocks={num_blocks}")
+    return block * int(block_size) + int(position) % int(block_size)

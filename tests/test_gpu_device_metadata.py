@@ -1,7 +1,9 @@
 """GPU checks of the device-resident block allocator and decode-step
-metadata against the host restatement of the reference's block manager and
-metadata builder (vpa.host.BlockManager and slot_for_block_table_position,
-themselves pinned by the reference's KATs in tests/test_host_metadata.py).
+metadata against the oracle's pure-Python restatement of the reference's
+block manager and slot rule (oracle.BlockManager, oracle.slot_for_position:
+paged_cache_runtime.rs:217-371, paged_kv_cache.rs:74-103; pinned by the
+reference's KATs in tests/test_oracle.py, and equal to the library's host
+block manager there).
 
 A batch is admitted (prompt blocks, row by row), then decoded step by step
 while rows finish (trim to their tokens, or free) and the pool runs dry (rows
@@ -14,7 +16,7 @@ import pytest
 import torch
 
 import vpa
-from vpa import host
+from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -34,7 +36,7 @@ def host_step(mgr, rids, pos, finished, bs, num_blocks):
             ctx.append(1)
             continue
         table = mgr.block_ids(rid)
-        slots.append(host.slot_for_block_table_position(table, bs, num_blocks, pos[r]))
+        slots.append(orc.slot_for_position(table, bs, num_blocks, pos[r]))
         ctx.append(pos[r] + 1)
         pos[r] += 1
     return np.array(slots, np.int64), np.array(ctx, np.uint32)
@@ -56,7 +58,7 @@ def test_device_allocator_follows_host_block_manager(device, graph):
     num_blocks, bs, batch, cols = 72, 16, 24, 24
     prompts = rng.integers(1, 60, size=batch)
     rids = list(range(100, 100 + batch))
-    mgr = host.BlockManager(num_blocks, bs)
+    mgr = orc.BlockManager(num_blocks, bs)
     alloc = vpa.DeviceBlockAllocator(num_blocks, bs, batch, cols, device)
 
     # admission: rows in order, as many as the pool holds
@@ -121,12 +123,12 @@ def test_admission_fits_then_overflows(device):
     """A first admission whose missing blocks all fit the ring (every row
     takes its blocks at once) and a second, growing the same rows, that does
     not (rows are served in order until the ring runs dry, later rows that
-    still fit succeed): tables, counts and ok flags equal the host block
-    manager's after each. (The host manager has no table width, so rows are
-    kept within the device tables' columns.)"""
+    still fit succeed): tables, counts and ok flags equal the oracle block
+    manager's after each. (The manager has no table width, so rows are kept
+    within the device tables' columns.)"""
     rng = np.random.default_rng(21)
     num_blocks, bs, batch, cols = 130, 16, 40, 12
-    mgr = host.BlockManager(num_blocks, bs)
+    mgr = orc.BlockManager(num_blocks, bs)
     alloc = vpa.DeviceBlockAllocator(num_blocks, bs, batch, cols, device)
     rids = list(range(batch))
     first = rng.integers(1, 50, size=batch)

@@ -129,14 +129,13 @@ def test_device_step_over_a_pool_that_runs_dry(device):
     """DeviceDecodeStep over a pool with a few spare blocks, so rows stall
     when their next token needs a block, and resume when finished rows free
     theirs; in lockstep with a host model of the same loop: the oracle's
-    step-start bookkeeping (with the stall rule), the host block manager and
-    metadata builder, the oracle's appends, the oracle's argmax. After every
+    step-start bookkeeping (with the stall rule), the oracle's block manager
+    and slot rule, the oracle's appends, the oracle's argmax. After every
     step the token state (generated lists, finished flags, input and
     pending ids), slots, context lengths, positions and tables must equal the
     host's; at the end both layers' caches bit for bit, and the last step's
     attention of every row that ran against the fp64 oracle."""
     from tests.test_gpu_device_metadata import check_same, host_step
-    from vpa import host
 
     rng = np.random.default_rng(23)
     b, nl, steps, cap = 20, 2, 22, 32
@@ -157,7 +156,7 @@ def test_device_step_over_a_pool_that_runs_dry(device):
     ok = st.admit(torch.from_numpy(prompts.astype(np.uint32)).to(device)).cpu().numpy()
 
     rids = list(range(b))
-    mgr = host.BlockManager(nb, BS)
+    mgr = orc.BlockManager(nb, BS)
     assert [mgr.try_allocate_slots(r, int(p)) for r, p in zip(rids, prompts)] == \
         ok.astype(bool).tolist() == [True] * b
     pos = [int(p) for p in prompts]

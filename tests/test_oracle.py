@@ -590,3 +590,95 @@ def test_consume_oracle_equals_reference_loop_with_compaction():
         nid = np.where(fin == 0, new_ids[s], nid).astype(np.uint32)  # forward + argmax
     assert fin.astype(bool).tolist() == want_fin
     assert [gen[i, :glen[i]].tolist() for i in range(batch)] == want_gen
+
+
+# ---- block manager restatement (paged_cache_runtime.rs:217-371) -------------
+
+def test_oracle_block_manager_reference_kats():
+    """The reference's own KATs (paged_cache_runtime.rs:737-778) on the
+    oracle's restatement."""
+    m = orc.BlockManager(8, 4)                      # :737-752
+    assert m.free_blocks() == 7
+    m.allocate_slots(10, 5)
+    assert len(m.block_ids(10)) == 2 and m.free_blocks() == 5
+    m.allocate_slots(10, 9)
+    assert len(m.block_ids(10)) == 3 and m.free_blocks() == 4
+    m.free_request(10)
+    assert m.free_blocks() == 7
+    m = orc.BlockManager(8, 4)                      # :755-769
+    m.allocate_slots(10, 12)
+    assert len(m.block_ids(10)) == 3 and m.free_blocks() == 4
+    m.trim_request_to_num_tokens(10, 5)
+    assert len(m.block_ids(10)) == 2 and m.free_blocks() == 5
+    m.trim_request_to_num_tokens(10, 1)
+    assert len(m.block_ids(10)) == 1 and m.free_blocks() == 6
+    m = orc.BlockManager(4, 4)                      # :772-778
+    assert m.try_allocate_slots(1, 4)
+    assert not m.try_allocate_slots(2, 16)
+    assert m.free_blocks() == 2
+    with pytest.raises(orc.OracleError, match="paged KV cache exhausted"):
+        m.allocate_slots(2, 16)
+    assert orc.BlockManager.allocatable_block_capacity(8) == 7
+
+
+def test_oracle_block_manager_free_list_order():
+    """FIFO hand-out from the front, freed and trimmed tails returned to the
+    back last block first (VecDeque push_back of the reversed tail,
+    paged_cache_runtime.rs:322-359); block 0 never handed out."""
+    m = orc.BlockManager(8, 4)
+    m.allocate_slots(1, 8)
+    m.allocate_slots(2, 4)
+    assert m.block_ids(1) == [1, 2] and m.block_ids(2) == [3]
+    m.free_request(1)
+    m.allocate_slots(3, 24)
+    assert m.block_ids(3) == [4, 5, 6, 7, 2, 1]
+    m.trim_request_to_num_tokens(3, 9)
+    m.allocate_slots(4, 12)
+    assert m.block_ids(4) == [1, 2, 7] and m.block_ids(3) == [4, 5, 6]
+    assert m.total_allocated_blocks() == 7 and m.free_blocks() == 0
+    assert m.slots_available_for(3, 12) and not m.slots_available_for(3, 13)
+    assert m.try_allocate_slots(5, 0) and m.blocks_for_request(5) == 0
+    with pytest.raises(orc.OracleError):
+        m.block_ids(99)
+    assert orc.slot_for_position([3, 9], 4, 10, 6) == 9 * 4 + 2
+    with pytest.raises(orc.OracleError, match="missing block table entry"):
+        orc.slot_for_position([3, 9], 4, 10, 8)
+    with pytest.raises(orc.OracleError, match="exceeds paged cache capacity"):
+        orc.slot_for_position([3, 12], 4, 10, 5)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_host_block_manager_equals_oracle_restatement(seed):
+    """The library's host block manager (C ABI, csrc/host_metadata.cpp) and
+    the oracle's pure-Python restatement stay equal through a random run of
+    grows, trims, frees and exhaustion."""
+    from vpa import host
+    rng = np.random.default_rng(seed)
+    nb, bs = 40, 8
+    a, b = host.BlockManager(nb, bs), orc.BlockManager(nb, bs)
+    tokens = {}
+    for _ in range(400):
+        rid = int(rng.integers(0, 12))
+        op = rng.random()
+        if op < 0.55:
+            n = tokens.get(rid, 0) + int(rng.integers(0, 3 * bs))
+            ok_a, ok_b = a.try_allocate_slots(rid, n), b.try_allocate_slots(rid, n)
+            assert ok_a == ok_b
+            if ok_a:
+                tokens[rid] = max(tokens.get(rid, 0), n)
+        elif op < 0.8:
+            n = int(rng.integers(0, tokens.get(rid, 0) + 1))
+            a.trim_request_to_num_tokens(rid, n)
+            b.trim_request_to_num_tokens(rid, n)
+            if rid in tokens:
+                tokens[rid] = min(tokens[rid], n)
+        else:
+            a.free_request(rid)
+            b.free_request(rid)
+            tokens.pop(rid, None)
+        assert a.free_blocks() == b.free_blocks()
+        assert a.total_allocated_blocks() == b.total_allocated_blocks()
+        for r in range(12):
+            assert a.blocks_for_request(r) == b.blocks_for_request(r)
+            if b.blocks_for_request(r):
+                assert a.block_ids(r) == b.block_ids(r)
