@@ -28,10 +28,13 @@
 // type for the MFMA; the row sums use the unrounded values. The output is
 // acc / sum without an epsilon, as flash attention computes it.
 //
-// Tile pipeline: a pipeline step is kPrefillSub tiles (two: one barrier,
-// one max exchange and one rescale test per 64 keys, which the fp8 path,
-// with its operand conversions, needs most; both cache types use the same
-// steps, so their rescale points, and with scales 1 their results, agree).
+// Tile pipeline: the online softmax works on groups of two tiles (one max
+// exchange and one rescale test per 64 keys); a pipeline step (one barrier,
+// one refill of the other stage buffer) is two tiles for 16-bit caches and
+// four for fp8, whose tiles are half the bytes, so two steps of four still
+// leave room for two workgroups per CU. Both cache types use the same
+// softmax groups, so their rescale points, and with scales 1 their
+// results, agree.
 // K and V tiles travel HBM -> LDS by the LDS-DMA form of the 16-byte global
 // load (no VGPR round trip) into two stage buffers; step t + 1 is issued
 // while step t is consumed, waits are explicit vmcnt counts plus a bare
@@ -91,12 +94,13 @@ __device__ __forceinline__ float max_xor32(float v) {
 #ifndef VPA_PREFILL_WAVES_PER_EU
 #define VPA_PREFILL_WAVES_PER_EU 2
 #endif
-#ifndef VPA_PREFILL_SUB
-#define VPA_PREFILL_SUB 2
-#endif
 constexpr int kPrefillKeys = 32;                    // keys per tile
-constexpr int kPrefillSub = VPA_PREFILL_SUB;        // tiles per pipeline step
-static_assert(kPrefillSub == 1 || kPrefillSub == 2, "tiles per step");
+constexpr int kSoftmaxTiles = 2;  // tiles per online-softmax group
+// tiles per pipeline step
+template <bool kF8>
+constexpr int prefill_step_tiles() {
+  return kF8 ? 4 : 2;
+}
 #ifndef VPA_PREFILL_WAVES
 #define VPA_PREFILL_WAVES 4
 #endif
@@ -264,7 +268,8 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   constexpr bool kF8 = std::is_same_v<C, fp8_t>;
   static_assert(kF8 || std::is_same_v<C, T>, "cache type is the query type or fp8");
   constexpr int KT = kPrefillKeys;
-  constexpr int SUB = kPrefillSub;
+  constexpr int SUB = prefill_step_tiles<kF8>();
+  static_assert(SUB % kSoftmaxTiles == 0, "whole softmax groups per step");
   constexpr int X = kF8 ? 16 : 8;  // cache elements per 16-byte unit
   constexpr int PPW = 32 / G;   // query positions per wave
   constexpr int PPB = kPrefillWaves * PPW;  // query positions per workgroup
@@ -455,7 +460,12 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
         const int b = di / DPB;
         uint32_t phys;
         if constexpr (NBT <= 2) {
-          phys = b == 0 ? pb[0] : pb[NBT - 1];
+          // (select between values, not between array elements: a select
+          // of two loads would become one runtime-indexed load and keep the
+          // block ids in scratch memory)
+          const uint32_t id0 = __builtin_amdgcn_readfirstlane(pb[0]);
+          const uint32_t id1 = __builtin_amdgcn_readfirstlane(pb[NBT - 1]);
+          phys = b == 0 ? id0 : id1;
         } else {
           // (a select over more blocks by the runtime index b becomes an
           // indexed scratch array: load the id from the table instead)
@@ -597,46 +607,51 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
         o[dt] = mfma32x32x16<T>(__builtin_bit_cast(uint4, vop[dt][k2]), pk[k2], o[dt]);
   };
 
-  // the SUB tiles of step t: scores of each, one online-softmax update for
-  // the step (on the raw scores; the scale is positive), then P.V of each
+  // the SUB tiles of step t in softmax groups of two: scores of both tiles
+  // of a group, one online-softmax update for the group (on the raw scores;
+  // the scale is positive), then P.V of each
   auto compute = [&](auto sc, int t, const uint32_t (&vmask)[SUB]) {
-    const int k0 = t * SUB * KT;
-    if (k0 >= wave_keys) return;  // no row of this wave sees these keys
-    f32x16_t sacc[SUB];
-    sacc[0] = scores(kst(sc, 0), k0, vmask[0]);
-    if constexpr (SUB == 2) {
-      if (k0 + KT < wave_keys) {
-        sacc[1] = scores(kst(sc, 1), k0 + KT, vmask[1]);
-      } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[1][r] = -INFINITY;
+    for (int g0 = 0; g0 < SUB; g0 += kSoftmaxTiles) {
+      const int k0 = (t * SUB + g0) * KT;
+      if (k0 >= wave_keys) return;  // no row of this wave sees these keys
+      f32x16_t sacc[kSoftmaxTiles];
+      sacc[0] = scores(kst(sc, g0), k0, vmask[g0]);
+#pragma unroll
+      for (int u = 1; u < kSoftmaxTiles; ++u) {
+        if (k0 + u * KT < wave_keys) {
+          sacc[u] = scores(kst(sc, g0 + u), k0 + u * KT, vmask[g0 + u]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[u][r] = -INFINITY;
+        }
       }
-    }
-    float mx = -INFINITY;
+      float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < SUB; ++u)
+      for (int u = 0; u < kSoftmaxTiles; ++u)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
-    mx = max_xor32(mx) * sl;
-    mt = fmaxf(mt, mx);
-    // The reference max m only moves when some row's step max exceeds it by
-    // more than kRescaleSlack (log2 units): the probabilities stay below
-    // 2^kRescaleSlack, and O and the row sums are rescaled only then.
-    constexpr float kRescaleSlack = 8.f;
-    if (__ballot(mx > m + kRescaleSlack) != 0) {
-      const float m_new = fmaxf(m, mx);
-      const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
-      lsum *= alpha;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
+      mx = max_xor32(mx) * sl;
+      mt = fmaxf(mt, mx);
+      // The reference max m only moves when some row's group max exceeds it
+      // by more than kRescaleSlack (log2 units): the probabilities stay below
+      // 2^kRescaleSlack, and O and the row sums are rescaled only then.
+      constexpr float kRescaleSlack = 8.f;
+      if (__ballot(mx > m + kRescaleSlack) != 0) {
+        const float m_new = fmaxf(m, mx);
+        const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
+        lsum *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-      m = m_new;
-    }
-    const float m_use = m == -INFINITY ? 0.f : m;  // a row without keys so far
-    accumulate(vst(sc, 0), sacc[0], m_use);
-    if constexpr (SUB == 2) {
-      if (k0 + KT < wave_keys) accumulate(vst(sc, 1), sacc[1], m_use);
+          for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+        m = m_new;
+      }
+      const float m_use = m == -INFINITY ? 0.f : m;  // a row without keys so far
+      accumulate(vst(sc, g0), sacc[0], m_use);
+#pragma unroll
+      for (int u = 1; u < kSoftmaxTiles; ++u)
+        if (k0 + u * KT < wave_keys) accumulate(vst(sc, g0 + u), sacc[u], m_use);
     }
   };
 
