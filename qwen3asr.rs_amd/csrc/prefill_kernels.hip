@@ -31,8 +31,8 @@
 // Tile pipeline: the online softmax works on groups of two tiles (one max
 // exchange and one rescale test per 64 keys); a pipeline step (one barrier,
 // one refill of the other stage buffer) is two tiles for 16-bit caches and
-// four for fp8, whose tiles are half the bytes, so two steps of four still
-// leave room for two workgroups per CU. Both cache types use the same
+// four for fp8 up to head_dim 128, whose tiles are half the bytes, so two
+// steps of four still leave room for two workgroups per CU. Both cache types use the same
 // softmax groups, so their rescale points, and with scales 1 their
 // results, agree.
 // K and V tiles travel HBM -> LDS by the LDS-DMA form of the 16-byte global
@@ -96,10 +96,12 @@ __device__ __forceinline__ float max_xor32(float v) {
 #endif
 constexpr int kPrefillKeys = 32;                    // keys per tile
 constexpr int kSoftmaxTiles = 2;  // tiles per online-softmax group
-// tiles per pipeline step
-template <bool kF8>
+// tiles per pipeline step: four for fp8 caches up to head_dim 128 with
+// blocks of 16 or 32 tokens (more block ids and DMA offsets per step would
+// not fit the scalar registers of the larger shapes), two otherwise
+template <bool kF8, int D, int BS>
 constexpr int prefill_step_tiles() {
-  return kF8 ? 4 : 2;
+  return kF8 && D <= 128 && BS >= 16 ? 4 : 2;
 }
 #ifndef VPA_PREFILL_WAVES
 #define VPA_PREFILL_WAVES 4
@@ -268,7 +270,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   constexpr bool kF8 = std::is_same_v<C, fp8_t>;
   static_assert(kF8 || std::is_same_v<C, T>, "cache type is the query type or fp8");
   constexpr int KT = kPrefillKeys;
-  constexpr int SUB = prefill_step_tiles<kF8>();
+  constexpr int SUB = prefill_step_tiles<kF8, D, BS>();
   static_assert(SUB % kSoftmaxTiles == 0, "whole softmax groups per step");
   constexpr int X = kF8 ? 16 : 8;  // cache elements per 16-byte unit
   constexpr int PPW = 32 / G;   // query positions per wave
@@ -505,12 +507,13 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
 
   // keys of tile t that exist: inside the context and in a present block
   // (uniform over the workgroup)
-  auto tile_mask = [&](int t, const uint32_t (&pb)[NBT]) {
+  // (present: bit kb set when block kb of the tile is inside the pool)
+  auto tile_mask = [&](int t, uint32_t present) {
     const int k0 = t * KT;
     uint32_t vmask = 0;
 #pragma unroll
     for (int kb = 0; kb < NBT; ++kb)
-      if ((int64_t)pb[kb] < num_blocks)
+      if ((present >> kb) & 1u)
         vmask |= (BS >= 32 ? 0xffffffffu : ((1u << BS) - 1u)) << (kb * BS);
     const int nk = k_len - k0;
     if (nk < KT) vmask &= (1u << max(nk, 0)) - 1u;
@@ -655,17 +658,43 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
     }
   };
 
+  // bit u NBT + kb: block kb of tile u of a step is inside the pool
+  const bool huge_pool = num_blocks > (int64_t)0xffffffffu;  // every u32 id is inside
+  auto step_present = [&](const uint32_t (&pbs)[SUB][NBT]) {
+    uint32_t bits = 0;
+#pragma unroll
+    for (int u = 0; u < SUB; ++u)
+#pragma unroll
+      for (int kb = 0; kb < NBT; ++kb)
+        if (huge_pool || pbs[u][kb] < (uint32_t)num_blocks) bits |= 1u << (u * NBT + kb);
+    return bits;
+  };
+  static_assert(SUB * NBT <= 32, "presence bits of a step");
+
   // one pipeline step: wait for step t's tiles, refill the stage step t-1
   // used with step t + 1, compute step t. The block ids travel ahead of the
-  // steps: pm (step t, for the masks) and pi (step t + 1, for the DMAs
-  // issued here) were loaded two steps and one step earlier, and the ids of
-  // step t + 2 are loaded into pf here, so no step waits for a table load.
-  auto step = [&](auto sc, int t, const uint32_t (&pm)[SUB][NBT],
-                  const uint32_t (&pi)[SUB][NBT], uint32_t (&pf)[SUB][NBT]) {
+  // steps: pi (step t + 1, for the DMAs issued here) was loaded one step
+  // earlier and the ids of step t + 2 are loaded into pf here, so no step
+  // waits for a table load; the masks of step t need only which of its
+  // blocks are inside the pool (pres, worked out when its DMAs were issued;
+  // pres_next gets step t + 1's).
+  // (With four blocks per tile the DMAs load their block ids from the table
+  // themselves and the registers of two steps' ids would not fit the larger
+  // shapes: each step then loads its own ids, before its waits, for the
+  // masks, and pi / pf are not used.)
+  constexpr bool kCarryIds = NBT <= 2;
+  auto step = [&](auto sc, int t, uint32_t pres, const uint32_t (&pi)[SUB][NBT],
+                  uint32_t (&pf)[SUB][NBT], uint32_t& pres_next) {
     if (t >= n_steps) return;
     constexpr int S = decltype(sc)::value;
     const bool refill = t + 1 < n_steps;
-    if (t + 2 < n_steps) step_blocks(t + 2, pf);
+    if constexpr (kCarryIds) {
+      if (t + 2 < n_steps) step_blocks(t + 2, pf);
+    } else {
+      uint32_t own[SUB][NBT];
+      step_blocks(t, own);
+      pres = step_present(own);
+    }
     wait_vmcnt<0>();  // step t's DMAs (the only ones in flight)
     // step t is in LDS for every wave, and every wave is done with step t-1.
     // A bare s_barrier: __syncthreads() would also fence this wave's LDS
@@ -678,7 +707,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
     bool fix = false;
 #pragma unroll
     for (int u = 0; u < SUB; ++u) {
-      vmask[u] = tile_mask(t * SUB + u, pm[u]);
+      vmask[u] = tile_mask(t * SUB + u, (pres >> (u * NBT)) & ((1u << NBT) - 1u));
       // tiles past the last one are read by no wave
       fix |= vmask[u] != 0xffffffffu && t * SUB + u < n_tiles;
     }
@@ -691,25 +720,24 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     }
-    if (refill) issue(Int<1 - S>{}, t + 1, pi);
+    if (refill) {
+      if constexpr (kCarryIds) pres_next = step_present(pi);
+      issue(Int<1 - S>{}, t + 1, pi);
+    }
     compute(sc, t, vmask);
   };
   if (n_steps > 0) {
-    // ids of steps t0 (a), t0 + 1 (b) and the one loaded two ahead (c)
-    uint32_t ia[SUB][NBT] = {}, ib[SUB][NBT] = {}, ic[SUB][NBT] = {};
-    step_blocks(0, ia);
-    issue(Int<0>{}, 0, ia);
-    if (1 < n_steps) step_blocks(1, ib);
+    // ids of the step whose DMAs come next (x at even steps, y at odd ones)
+    // and of the one after it; presence bits of the current and next step
+    uint32_t ix[SUB][NBT] = {}, iy[SUB][NBT] = {};
+    uint32_t p0 = 0, p1 = 0;
+    step_blocks(0, ix);
+    p0 = step_present(ix);
+    issue(Int<0>{}, 0, ix);
+    if (kCarryIds && 1 < n_steps) step_blocks(1, ix);
     for (int t0 = 0; t0 < n_steps; t0 += 2) {
-      step(Int<0>{}, t0, ia, ib, ic);      // loads the ids of t0 + 2 into ic
-      step(Int<1>{}, t0 + 1, ib, ic, ia);  // loads the ids of t0 + 3 into ia
-#pragma unroll
-      for (int u = 0; u < SUB; ++u)
-#pragma unroll
-        for (int i = 0; i < NBT; ++i) {
-          ib[u][i] = ia[u][i];
-          ia[u][i] = ic[u][i];
-        }
+      step(Int<0>{}, t0, p0, ix, iy, p1);      // loads the ids of t0 + 2 into iy
+      step(Int<1>{}, t0 + 1, p1, iy, ix, p0);  // loads the ids of t0 + 3 into ix
     }
   }
 
