@@ -643,7 +643,9 @@ def traffic_from_profile(w):
 def decode_seeds(dev, seeds, reps, warmup):
     """The c3 decode over several seeds of its generation rule (each seed
     draws its own lengths and tables): decode alone and inside the step, us
-    per layer and fraction of the HBM peak, with each seed's mean context."""
+    per layer and fraction of the HBM peak, with each seed's mean context,
+    and the read-only pass over the seed's tiles with the decode's fraction
+    of it."""
     import numpy as np
     import torch
 
@@ -657,7 +659,8 @@ def decode_seeds(dev, seeds, reps, warmup):
         ws = vpa.paged_attention_workspace(w.num_seqs, w.num_heads, w.head_dim,
                                            w.max_context_len, dev)
         run_step(layers, ctx, w, ws)
-        t = op_timings(layers, ctx, w, ws, reps, warmup)
+        sink = torch.zeros(1, dtype=torch.uint32, device=dev)
+        t = op_timings(layers, ctx, w, ws, reps, warmup, sink=sink)
         b = w.decode_bytes_per_layer()
         rows.append({
             "seed": sd,
@@ -667,6 +670,9 @@ def decode_seeds(dev, seeds, reps, warmup):
             "decode_in_step_us": round(t["decode_in_step"], 2),
             "decode_in_step_frac_of_peak": round(
                 b / (t["decode_in_step"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+            "read_us": round(t["read"], 2),
+            "read_frac_of_peak": round(b / (t["read"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+            "decode_frac_of_measured": round(t["read"] / t["decode"], 4),
         })
         del layers, ws, ctx
         torch.cuda.empty_cache()
@@ -675,6 +681,7 @@ def decode_seeds(dev, seeds, reps, warmup):
         "seeds": rows,
         "min_decode_frac_of_peak": min(r["decode_frac_of_peak"] for r in rows),
         "min_decode_in_step_frac_of_peak": min(r["decode_in_step_frac_of_peak"] for r in rows),
+        "min_decode_frac_of_measured": min(r["decode_frac_of_measured"] for r in rows),
     }
 
 
