@@ -261,6 +261,15 @@ def fp8_prefill_case(device, code, h, kvh, bs, prior, qlens, seed, causal=True,
     return orc.to_f32(to_host(out), code), want, (q, kc, vc, bt, lens32, cu, scale)
 
 
+@pytest.mark.parametrize("bs", [8, 16])
+def test_fp8_prefill_long_context(device, bs):
+    """16 000 prior tokens over an fp8 cache: four-tile steps walked ~125
+    times at 16-token blocks, per-step block-id loads at 8-token blocks."""
+    got, want, _ = fp8_prefill_case(device, orc.BF16, 16, 8, bs, [16000, 40], [160, 24],
+                                    seed=33)
+    assert_attention_close(got, want, orc.BF16, f"fp8 prefill long context bs={bs}")
+
+
 PF_PRIOR = [0, 5, 31, 100, 0, 333]
 PF_NEW = [1, 31, 32, 33, 129, 70]
 

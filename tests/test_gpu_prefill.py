@@ -216,6 +216,26 @@ def test_prefill_max_query_len_clamps_rows(device):
     assert_attention_close(got[50:], want1, code, "seq 1")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+def test_prefill_long_context(device, code, causal):
+    """A 16 000-token prior (1000 blocks; the last query tile walks ~250
+    two-tile steps) beside a short sequence: the block-id windows near the
+    table's end, the lazy rescale and the tail masks over a long run."""
+    got, want = prefill_case(device, code, 16, 8, 128, 16, [16000, 40], [160, 24], seed=31,
+                             causal=causal)
+    assert_attention_close(got, want, code, "long context")
+
+
+def test_prefill_long_context_large_scale(device):
+    """Logits ten times larger than the usual scale give (log2) spreads far
+    beyond the rescale slack: the reference max moves many times along a
+    12 000-token context."""
+    got, want = prefill_case(device, orc.BF16, 16, 8, 128, 16, [12000], [96], seed=32,
+                             scale=10 * 128 ** -0.5)
+    assert_attention_close(got, want, orc.BF16, "long context, scale 10/sqrt(d)")
+
+
 def test_prefill_config_c4_sampled(device):
     """c4 end to end on the GPU: append the 512 new tokens of each of the 64
     sequences with reshape_and_cache, then prefill; eight sequences are
