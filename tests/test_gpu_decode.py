@@ -187,6 +187,16 @@ def test_decode_long_context_split_k(device):
     assert_attention_close(got, want, orc.BF16, "long")
 
 
+@pytest.mark.parametrize("code", [orc.BF16, orc.F32])
+def test_decode_very_long_context_many_chunks(device, code):
+    """A 65 536-token context (32 chunks of the work list, 32 partial rows
+    merged) beside short and one-chunk ones; f32 runs the generic split-K
+    kernel over the same lengths."""
+    lens = [65536, 40001, 2048, 2049, 1]
+    got, want = decode_case(device, code, 16, 8, 128, 16, lens, seed=78)
+    assert_attention_close(got, want, code, f"very long code={code}")
+
+
 def test_decode_max_context_len_above_lengths_and_padded_columns(device):
     """max_context_len frozen above every length (graph-capture style) and
     block tables padded with 0 columns (paged_kv_cache.rs:954-964) or a
