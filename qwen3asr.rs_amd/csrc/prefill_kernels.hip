@@ -384,6 +384,9 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   const C* vbase = value_cache + (int64_t)j * head_stride;
   const uint32_t* bt = block_tables + (int64_t)s * block_table_stride;
   const int last_blk = max(k_len - 1, 0) / BS;
+  // every u32 block id is inside the pool (the id checks compare 32 bits,
+  // in scalar registers, otherwise)
+  const bool huge_pool = num_blocks > (int64_t)0xffffffffu;
 
   // K and V regions of tile u of stage S
   auto kst = [&](auto sc, int u) -> uint4* {
@@ -473,7 +476,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
           // indexed scratch array: load the id from the table instead)
           phys = bt[__builtin_amdgcn_readfirstlane(min(k0 / BS + b, last_blk))];
         }
-        phys = (k0 + b * BS < k_len && (int64_t)phys < num_blocks) ? phys : 0u;
+        phys = (k0 + b * BS < k_len && (huge_pool || phys < (uint32_t)num_blocks)) ? phys : 0u;
         phys = __builtin_amdgcn_readfirstlane(phys);
         const int64_t blk = (int64_t)phys * block_stride;
         dma16(kbase + blk + koff[i], sk + b * RBK + (di % DPB) * 64);
@@ -618,17 +621,13 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
     for (int g0 = 0; g0 < SUB; g0 += kSoftmaxTiles) {
       const int k0 = (t * SUB + g0) * KT;
       if (k0 >= wave_keys) return;  // no row of this wave sees these keys
+      // (every tile of the group is scored: one past this wave's keys is
+      // masked whole, which is cheaper than the -inf fill the compiler would
+      // otherwise hoist into the common path)
       f32x16_t sacc[kSoftmaxTiles];
-      sacc[0] = scores(kst(sc, g0), k0, vmask[g0]);
 #pragma unroll
-      for (int u = 1; u < kSoftmaxTiles; ++u) {
-        if (k0 + u * KT < wave_keys) {
-          sacc[u] = scores(kst(sc, g0 + u), k0 + u * KT, vmask[g0 + u]);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sacc[u][r] = -INFINITY;
-        }
-      }
+      for (int u = 0; u < kSoftmaxTiles; ++u)
+        sacc[u] = scores(kst(sc, g0 + u), k0 + u * KT, vmask[g0 + u]);
       float mx = -INFINITY;
 #pragma unroll
       for (int u = 0; u < kSoftmaxTiles; ++u)
@@ -659,7 +658,6 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   };
 
   // bit u NBT + kb: block kb of tile u of a step is inside the pool
-  const bool huge_pool = num_blocks > (int64_t)0xffffffffu;  // every u32 id is inside
   auto step_present = [&](const uint32_t (&pbs)[SUB][NBT]) {
     uint32_t bits = 0;
 #pragma unroll
