@@ -16,7 +16,8 @@
 // and the host reads one 4-byte active count only when it wants to stop.
 //
 // argmax_rows_kernel: one 1024-thread workgroup per row; 16-byte loads of the
-// row, a per-thread best (value, index), then wave and workgroup reductions.
+// row (four in flight per thread), a per-thread best (value, index), then
+// wave and workgroup reductions.
 // Candle's argmax scans left to right and moves only on a strictly greater
 // value: the first maximum wins, a NaN is never taken after element 0, and
 // a NaN at element 0 is never left. The reduction keeps exactly that order:
@@ -60,14 +61,24 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(
   };
   int v0 = 0;
   if (vec_ok) {
+    // four non-temporal 16-byte loads in flight per thread (the logits are
+    // read once); the result does not depend on the order of the takes
     const int nvec = vocab / X;
     const uint4* rv = reinterpret_cast<const uint4*>(row);
-    for (int q = tid; q < nvec; q += kArgmaxThreads) {
-      const uint4 u = rv[q];
+    auto take_vec = [&](const uint4& u, int q) {
       const T* e = reinterpret_cast<const T*>(&u);
 #pragma unroll
       for (int k = 0; k < X; ++k) take(load_as_f32(e + k), (uint32_t)(q * X + k));
+    };
+    int q = tid;
+    for (; q + 3 * kArgmaxThreads < nvec; q += 4 * kArgmaxThreads) {
+      uint4 u[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) u[j] = load_stream(rv + q + j * kArgmaxThreads);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) take_vec(u[j], q + j * kArgmaxThreads);
     }
+    for (; q < nvec; q += kArgmaxThreads) take_vec(load_stream(rv + q), q);
     v0 = nvec * X;
   }
   for (int i = v0 + tid; i < vocab; i += kArgmaxThreads) take(load_as_f32(row + i), (uint32_t)i);
