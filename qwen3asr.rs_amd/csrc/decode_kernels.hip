@@ -328,8 +328,8 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
 //     a row are summed with DPP once at the end.
 // The NW partial results are merged in LDS. A sequence of a single chunk
 // writes its output directly; a longer one writes one f32 partial row per
-// chunk (D values + a 32-float line holding {max, sum}, whole 128-byte
-// lines), merged by decode_merge_kernel over the plan's list of multi-chunk
+// chunk (D values + a 32-float line holding {max (log2 units), sum}, whole
+// 128-byte lines), merged by decode_merge_kernel over the plan's list of multi-chunk
 // sequences. (Merging in the last workgroup to finish would need an
 // agent-scope release per chunk, which on gfx950 writes back the XCD's L2:
 // measured with only that fence added, c3 decode went from 176 to 823 us
@@ -571,6 +571,10 @@ void paged_decode_rows_kernel(
     scale *= *k_scale;
     vs = *v_scale;
   }
+  // logits are kept in log2 units (scale * log2 e folded in), so every
+  // exponential below is one v_exp_f32; the partial rows' maxima are in the
+  // same units for decode_merge_kernel
+  scale *= 1.4426950408889634f;
 
   if (nb > 0) {
     // block ids of the partition (lane b holds block b) and this lane's q chunks
@@ -777,7 +781,8 @@ void paged_decode_rows_kernel(
         float sm = 0.f;
 #pragma unroll
         for (int i = 0; i < NPL; ++i) {
-          const float p = v[i] == -INFINITY ? 0.f : expf(v[i] - mx);
+          if (i * 64 >= ntok) break;  // (uniform) the P.V pass reads only the first ntok
+          const float p = v[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(v[i] - mx);
           sm += p;
           T pt;
           store_from_f32<T>(&pt, p);
@@ -849,7 +854,7 @@ void paged_decode_rows_kernel(
     float num = 0.f, den = 0.f;
 #pragma unroll
     for (int q = 0; q < NW; ++q) {
-      const float wq = s_m[q][g] == -INFINITY ? 0.f : expf(s_m[q][g] - mx);
+      const float wq = s_m[q][g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[q][g] - mx);
       num = fmaf(wq, s_logit[q][0][g * D + d], num);
       den = fmaf(wq, s_l[q][g], den);
     }
@@ -977,13 +982,13 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
 #pragma unroll
       for (int r = 0; r < R; ++r) cm = fmaxf(cm, pm[r]);
       if (cm == -INFINITY) continue;  // no token in these partials
-      const float rescale = mx == -INFINITY ? 0.f : expf(mx - cm);
+      const float rescale = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mx - cm);
       tot *= rescale;
 #pragma unroll
       for (int k = 0; k < DPL; ++k) a[k] *= rescale;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float wgt = pm[r] == -INFINITY ? 0.f : expf(pm[r] - cm);
+        const float wgt = pm[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[r] - cm);
         tot = fmaf(wgt, pl[r], tot);
 #pragma unroll
         for (int k = 0; k < DPL; ++k) a[k] = fmaf(wgt, v[r][k], a[k]);
