@@ -519,7 +519,12 @@ void paged_decode_rows_kernel(
   __shared__ float s_m[NW][G], s_l[NW][G];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Uniform where a stage holds at most two tiles: the partition bounds,
+  // block ids and tile addresses derived from the wave index then stay in
+  // scalar registers (with more tiles per stage their addresses would not
+  // fit them and spill).
+  const int wave = BKS <= 2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)
+                            : (int)(threadIdx.x >> 6);
   const uint32_t w = blockIdx.x;
   const int j = (int)(w % (uint32_t)num_kv_heads);
   const uint32_t want = w / (uint32_t)num_kv_heads;  // index of this workgroup's item
@@ -606,10 +611,13 @@ void paged_decode_rows_kernel(
     // Block id of tile u of stage st (uniform); blocks past the partition
     // or out of the pool read block 0 (in bounds) and are masked when
     // consumed, so loads never branch.
+    // (the pool check compares 32 bits, in scalar registers, unless the
+    // pool holds more than 2^32 blocks)
+    const bool huge_pool = num_blocks > (int64_t)0xffffffffu;
     auto tile_block = [&](int st, int u, bool& ok) -> uint32_t {
       const int bi = st * BKS + u;
       const uint32_t phys = (uint32_t)__builtin_amdgcn_readlane((int)my_bt, bi < nb ? bi : 0);
-      ok = bi < nb && (int64_t)phys < num_blocks;
+      ok = bi < nb && (huge_pool || phys < (uint32_t)num_blocks);
       return ok ? phys : 0u;
     };
     auto load_stage = [&](const uint4* base, int st, uint4(&buf)[NV]) {
