@@ -132,6 +132,11 @@ def pa_call(**over):
     (dict(), _lib.VPA_ERR_WORKSPACE, "workspace"),
     (dict(ws=FAKE + 16, ws_bytes=1 << 30), _lib.VPA_ERR_INVALID_ARGUMENT, "256-byte"),
     (dict(max_ctx=1 << 30, bts=1 << 26), _lib.VPA_ERR_UNSUPPORTED, "max_context_len"),
+    # one token past the longest context the split-K workspace holds
+    # (2048 partitions of 128 tokens)
+    (dict(max_ctx=262145, bts=1 << 15), _lib.VPA_ERR_UNSUPPORTED, "max_context_len"),
+    # the longest context passes the size checks and then needs its workspace
+    (dict(max_ctx=262144, bts=1 << 14), _lib.VPA_ERR_WORKSPACE, "workspace"),
 ])
 def test_paged_attention_host_validation(over, code, needle):
     rc, msg = pa_call(**over)

@@ -197,6 +197,17 @@ def test_decode_very_long_context_many_chunks(device, code):
     assert_attention_close(got, want, code, f"very long code={code}")
 
 
+@pytest.mark.parametrize("code", [orc.BF16, orc.F32])
+def test_decode_longest_supported_context(device, code):
+    """A context of exactly 262 144 tokens, the longest the split-K workspace
+    holds (2048 partitions of 128 tokens; one token more is rejected on the
+    host): 128 work-list chunks merged for bf16, 2048 partitions reduced by
+    the generic kernel for f32, beside a one-token and a two-chunk sequence."""
+    lens = [262144, 1, 2049]
+    got, want = decode_case(device, code, 2, 1, 128, 16, lens, seed=91)
+    assert_attention_close(got, want, code, f"longest context code={code}")
+
+
 def test_decode_max_context_len_above_lengths_and_padded_columns(device):
     """max_context_len frozen above every length (graph-capture style) and
     block tables padded with 0 columns (paged_kv_cache.rs:954-964) or a

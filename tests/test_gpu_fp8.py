@@ -165,6 +165,15 @@ def test_fp8_decode_chunk_and_wave_boundaries(device, bs):
     assert_attention_close(got, want, orc.BF16, f"fp8 edges bs={bs}")
 
 
+def test_fp8_decode_longest_supported_context(device):
+    """A 262 144-token context over an fp8 cache (the longest the decode
+    takes: 128 chunks merged) beside a one-token sequence, with scales."""
+    lens = [262144, 1]
+    got, want = fp8_decode_case(device, orc.BF16, 2, 1, 128, 16, lens, seed=93,
+                                scales=(0.6, 1.7))
+    assert_attention_close(got, want, orc.BF16, "fp8 longest context")
+
+
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("h,kvh", [(8, 8), (16, 8), (16, 4)])
 def test_fp8_decode_head_dims_and_groups(device, d, h, kvh):
