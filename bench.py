@@ -379,6 +379,9 @@ def device_step(w, dev, reps, warmup):
     for _ in range(warmup):
         g_full.replay()
     dev_ms = timed_ms(g_full.replay, reps)
+    # the same graph's device work alone (work list, layers, argmax) over the
+    # same tables and lengths: what the on-device bookkeeping and metadata add
+    work_ms = timed_ms(g_work.replay, reps)
 
     # host-driven: the host block manager follows the device allocator's state
     mgr = host.BlockManager(nb, BS)
@@ -432,11 +435,14 @@ def device_step(w, dev, reps, warmup):
     torch.cuda.empty_cache()
     return {"workload": w.name, "layers": len(w.layers), "vocab": vocab,
             "device_resident_ms_per_step": round(dev_ms, 4),
+            "device_work_only_ms_per_step": round(work_ms, 4),
             "host_driven_ms_per_step": round(host_ms, 4),
             "what": "one decode step: bookkeeping + block growth + metadata + work list + "
                     "28 x (append + attention) + argmax; device-resident = one graph replay "
-                    "per step, no host read; host-driven = ids read back, host bookkeeping and "
-                    "block manager, metadata upload, then a graph of the device work"}
+                    "per step, no host read; device work only = the same graph without the "
+                    "bookkeeping and metadata kernels; host-driven = ids read back, host "
+                    "bookkeeping and block manager, metadata upload, then a graph of the device "
+                    "work"}
 
 
 def prefill_c4(dev, reps=20, warm_s=0.25):
