@@ -695,7 +695,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
-              "paged-KV path is measured per GPU, see DESIGN.md for how it would shard",
+              "paged-KV path is measured on one GPU's share: decode and prefill shard by "
+              "sequence or by kv head with no exchange inside attention",
               file=sys.stderr)
         sys.exit(2)
 

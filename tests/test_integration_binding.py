@@ -1,4 +1,4 @@
-"""The Rust binding shown in INTEGRATION.md against include/vpa.h (CPU).
+"""The documented Rust binding for vasr-paged-attn against include/vpa.h (CPU).
 
 The `extern "C"` block a maintainer would add to vasr-paged-attn must
 declare every entry point of the C header with the same parameters, in the
