@@ -22,8 +22,9 @@
 namespace vpa {
 namespace {
 
-// 64 MiB: the rows-kernel layout of every BASELINE decode shape fits (c3:
-// 5.3 MB, c5 with batch 1024 and contexts up to 8192: 42 MB).
+// 64 MiB: the rows-kernel layout of every benchmark decode shape of this
+// package fits (c3, batch 256 with contexts up to 4000: 5.3 MB; c5, batch
+// 1024 with contexts up to 8192: 42 MB).
 constexpr size_t kScratchBytes = (size_t)64 << 20;
 
 // The library's decode scratch. In host code `scratch` names a host-side
