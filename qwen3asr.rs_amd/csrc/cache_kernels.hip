@@ -163,11 +163,8 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
     return;
   }
 
-  // General path: arbitrary slot per token. Value stores run along the token
-  // axis, so that tokens sharing a block write adjacent bytes, unless every
-  // token sits alone in its block (decode): then along the dims of one token,
-  // so that consecutive lanes write consecutive dim rows of its value tile
-  // (four to a 128-byte line at 16-token blocks of 2-byte values).
+  // General path: arbitrary slot per token. Lanes run along the token axis so
+  // that tokens sharing a block still produce adjacent addresses.
   // No two neighbouring tokens of the workgroup share a block (decode: one
   // token per sequence). Only neighbours are compared: tokens that share a
   // block without being adjacent (slots 5, 100, 6) also take the streaming
@@ -193,9 +190,8 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
     }
     const C* vsrc = reinterpret_cast<const C*>(v_rows);
     for (int i = tid; i < D * BS; i += kThreads) {
-      constexpr bool alone = decltype(streaming)::value;
-      const int d = alone ? i % D : i / BS;
-      const int t = alone ? i / D : i - d * BS;
+      const int d = i / BS;
+      const int t = i - d * BS;
       const int64_t s = slots[t];
       if (s >= 0) {
         const int64_t blk = s / BS;
