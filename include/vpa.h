@@ -214,8 +214,10 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
  * callers that cannot allocate device memory (code under HIP graph capture
  * that must not allocate, tight serving loops, harnesses that forbid
  * hipMalloc). The split-K partials and the work list live in a static
- * device array of the library, 64 MiB per GPU, held until the process ends
- * and laid out for the kernel this configuration runs (16-bit / fp8 caches
+ * device array of the library, 64 MiB per GPU (build-time
+ * VPA_NOALLOC_SCRATCH_MIB; `make NOALLOC_SCRATCH_MIB=<n>`), held until the
+ * process ends by every process that loads the library, whether or not it
+ * calls this entry point, and laid out for the kernel this configuration runs (16-bit / fp8 caches
  * with head_dim <= 128: num_seqs * num_heads * ceil(max_context_len / 2048)
  * partial rows of (head_dim + 32) floats, 5.3 MB at batch 256 / context
  * 4096, 42 MB at batch 1024 / context 8192). A call whose layout does not

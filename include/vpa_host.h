@@ -47,7 +47,12 @@ int vpa_pool_blocks_for_byte_budget(uint64_t byte_budget, uint64_t bytes_per_blo
 /* Pool blocks for `fraction` of the current device's memory: budget =
  * floor(total_MiB * fraction) - used_MiB (in MiB, from hipMemGetInfo), then
  * vpa_pool_blocks_for_byte_budget. PagedCacheMemory::GpuMemoryFraction
- * (paged_cache_runtime.rs:136-150, which reads nvidia-smi). */
+ * (paged_cache_runtime.rs:136-150, which reads nvidia-smi). The library's
+ * device code is loaded on the current device before the free memory is
+ * read, so used_MiB already counts the static decode scratch of
+ * vpa_paged_attention_noalloc (64 MiB per GPU by default, build-time
+ * VPA_NOALLOC_SCRATCH_MIB), which every process that loads the library holds
+ * on each GPU it runs on. */
 int vpa_pool_blocks_for_memory_fraction(float fraction, uint64_t bytes_per_block,
                                         int64_t* num_blocks);
 

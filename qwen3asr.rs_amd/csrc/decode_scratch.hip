@@ -22,10 +22,17 @@
 namespace vpa {
 namespace {
 
-// 64 MiB: the rows-kernel layout of every benchmark decode shape of this
-// package fits (c3, batch 256 with contexts up to 4000: 5.3 MB; c5, batch
-// 1024 with contexts up to 8192: 42 MB).
-constexpr size_t kScratchBytes = (size_t)64 << 20;
+// VPA_NOALLOC_SCRATCH_MIB (build-time, default 64): the rows-kernel layout
+// of every benchmark decode shape of this package fits 64 MiB (c3, batch 256
+// with contexts up to 4000: 5.3 MB; c5, batch 1024 with contexts up to 8192:
+// 42 MB). Every process that loads the library holds this much of each GPU
+// it runs on, whether or not it calls the allocation-free entry point.
+#ifndef VPA_NOALLOC_SCRATCH_MIB
+#define VPA_NOALLOC_SCRATCH_MIB 64
+#endif
+static_assert(VPA_NOALLOC_SCRATCH_MIB >= 1 && VPA_NOALLOC_SCRATCH_MIB <= 4096,
+              "VPA_NOALLOC_SCRATCH_MIB out of range");
+constexpr size_t kScratchBytes = (size_t)VPA_NOALLOC_SCRATCH_MIB << 20;
 
 // The library's decode scratch. In host code `scratch` names a host-side
 // stand-in: its device address comes from hipGetSymbolAddress, per device.
@@ -61,6 +68,14 @@ int scratch_address(const char* op, void** out) {
 }
 
 }  // namespace
+
+size_t noalloc_scratch_bytes() { return kScratchBytes; }
+
+int load_device_code(const char* op) {
+  void* p = nullptr;
+  return scratch_address(op, &p);
+}
+
 }  // namespace vpa
 
 using namespace vpa;

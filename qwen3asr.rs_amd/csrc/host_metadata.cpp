@@ -16,6 +16,7 @@
 
 #include "../../include/vpa_host.h"
 #include "vpa_internal.h"
+#include "vpa_internal.h"
 
 struct vpa_block_manager {
   int32_t block_size = 0;
@@ -187,6 +188,11 @@ int vpa_pool_blocks_for_memory_fraction(float fraction, uint64_t bytes_per_block
   if (!(fraction > 0.f && fraction <= 1.f))
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: GPU memory fraction must be in (0.0, 1.0]; got %g",
                 op, (double)fraction);
+  // the library's device code (and with it the static decode scratch of the
+  // allocation-free entry point) is loaded first, so that the free memory
+  // read below already excludes it
+  const int rc_load = vpa::load_device_code(op);
+  if (rc_load != VPA_OK) return rc_load;
   size_t free_b = 0, total_b = 0;
   const hipError_t e = hipMemGetInfo(&free_b, &total_b);
   if (e != hipSuccess)

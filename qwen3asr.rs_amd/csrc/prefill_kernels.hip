@@ -208,44 +208,44 @@ __device__ __forceinline__ constexpr int tile_key_of_row(int i) {
   return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
 }
 
-// s_waitcnt lgkmcnt(0) that the N registers just read from LDS (by the inline
-// ds_read above) depend on. At the head dims 64 and 128 the wait names them
-// all; otherwise it names the first few and an empty statement per other
-// register keeps every later use of it behind the wait.
-template <typename V, int N>
-__device__ __forceinline__ void lgkm_wait(V (&r)[N]) {
-  if constexpr (N == 4) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
-  } else if constexpr (N == 8) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
-                 "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
+// s_waitcnt lgkmcnt(0) that every one of the M registers just read from LDS
+// (by the inline ds_read above) depends on: each is an in-out operand of the
+// wait, so no use of it, a register copy included, can be placed before the
+// wait. M is 4, 6, 8, 12 or 16 (KS or 2 DT operands at head dims 64 to 256).
+template <typename V, int M>
+__device__ __forceinline__ void lgkm_wait_flat(V* r) {
+  static_assert(M == 4 || M == 6 || M == 8 || M == 12 || M == 16, "operand count");
+  if constexpr (M == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+  } else if constexpr (M == 6) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
+                   "+v"(r[4]), "+v"(r[5]));
+  } else if constexpr (M == 8) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
+                   "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
+  } else if constexpr (M == 12) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
+                   "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+                   "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]));
   } else {
-    static_assert(N > 4, "operand count");
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
-#pragma unroll
-    for (int i = 4; i < N; ++i) asm volatile("" : "+v"(r[i]));
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
+                   "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+                   "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]),
+                   "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15]));
   }
 }
 template <typename V, int N>
+__device__ __forceinline__ void lgkm_wait(V (&r)[N]) {
+  lgkm_wait_flat<V, N>(r);
+}
+template <typename V, int N>
 __device__ __forceinline__ void lgkm_wait(V (&r)[N][2]) {
-  if constexpr (N == 2) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(r[0][0]), "+v"(r[0][1]), "+v"(r[1][0]), "+v"(r[1][1]));
-  } else if constexpr (N == 4) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(r[0][0]), "+v"(r[0][1]), "+v"(r[1][0]), "+v"(r[1][1]), "+v"(r[2][0]),
-                   "+v"(r[2][1]), "+v"(r[3][0]), "+v"(r[3][1]));
-  } else {
-    static_assert(N == 3 || N > 4, "operand count");
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(r[0][0]), "+v"(r[0][1]), "+v"(r[1][0]), "+v"(r[1][1]), "+v"(r[2][0]),
-                   "+v"(r[2][1]));
-#pragma unroll
-    for (int i = 3; i < N; ++i) {
-      asm volatile("" : "+v"(r[i][0]));
-      asm volatile("" : "+v"(r[i][1]));
-    }
-  }
+  lgkm_wait_flat<V, 2 * N>(&r[0][0]);
 }
 
 // Waves per SIMD the kernel is built for: two up to head_dim 128; above,

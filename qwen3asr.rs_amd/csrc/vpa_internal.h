@@ -55,6 +55,13 @@ struct DecodeScratch {
   int (*address)(const char* op, void** out);
 };
 
+// Bytes of the static decode scratch on each GPU (VPA_NOALLOC_SCRATCH_MIB).
+size_t noalloc_scratch_bytes();
+// Loads this library's device code object on the current device (the HIP
+// runtime loads it lazily, and with it reserves the static decode scratch)
+// by looking up the scratch's address; VPA_OK or a HIP error status.
+int load_device_code(const char* op);
+
 // vpa_paged_attention and its variants: every argument check, then the
 // launches. With `scratch` the workspace arguments are ignored: after the
 // checks the call takes the library's scratch, laid out for the kernel that
