@@ -209,6 +209,60 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
                                 size_t workspace_bytes, void* stream);
 
 /*
+ * reshape_and_cache_paged_attention — one decode layer's two calls behind
+ * one entry point: reshape_and_cache of the step's new K/V rows
+ * (thinker_text.rs:1101-1109) followed by paged_attention
+ * (thinker_text.rs:1126-1139), for the decode step where each sequence
+ * appends one token at the last position of its context: row s of `key` /
+ * `value` ([num_seqs, num_kv_heads, head_dim] of the query type, token
+ * strides in elements, heads contiguous) is written at position
+ * context_lens[s] - 1 of sequence s's block table, the slot vASR's decode
+ * metadata gives that token (paged_kv_cache.rs:985-1017; graph pad rows,
+ * context 1 over table row 0, write block 0 offset 0 as slot 0 does). No
+ * counterpart in the reference. The results are those of the two calls
+ * with that slot mapping, bit for bit (cache bytes and output), provided
+ * that no two sequences' last positions share a cache block (vASR's block
+ * manager gives each request its own blocks; pad rows share block 0, whose
+ * token 0 then holds one of theirs, and each pad row's output is computed
+ * over its own token, where the two calls would give all of them the
+ * stored one). A sequence with context_lens[s] = 0, or a context that
+ * max_context_len or the table clamps, appends nothing.
+ * With bf16 / f16 caches (the query's type), head_dim 128 with blocks of 16
+ * or 32 tokens or head_dim 64 with 32 (a (block, head) tile of at least
+ * 2 KiB) and at most 48 sequences, the append runs inside the decode launch: the wave that
+ * reads a sequence's last block puts the new token into the K and V tiles
+ * it holds and writes whole 32-byte sectors back (the value tile whole, the
+ * key units of the token and its sector neighbour). Otherwise (larger
+ * batches, where those writes cost the bandwidth-bound decode more than the
+ * append's own launch; f32 and fp8 caches; other head dims) it launches the
+ * append kernel on the derived slots, then the decode. Arguments and errors
+ * as vpa_reshape_and_cache and vpa_paged_attention (dtype: the query and
+ * row type; scales as there); softcapping off, no alibi, no sinks.
+ */
+int vpa_reshape_and_cache_paged_attention(
+    void* out, const void* query, const void* key, const void* value, int64_t key_token_stride,
+    int64_t value_token_stride, const float* k_scale, const float* v_scale, void* key_cache,
+    void* value_cache, const uint32_t* block_tables, int32_t block_table_stride,
+    const uint32_t* context_lens, int32_t max_context_len, float softmax_scale, int32_t num_seqs,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int64_t num_blocks, int64_t cache_block_stride, int64_t cache_head_stride, int32_t dtype,
+    int32_t cache_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * reshape_and_cache_paged_attention_planned — the same without the
+ * work-list launch, over the list vpa_paged_attention_plan built (the
+ * conditions of vpa_paged_attention_planned).
+ */
+int vpa_reshape_and_cache_paged_attention_planned(
+    void* out, const void* query, const void* key, const void* value, int64_t key_token_stride,
+    int64_t value_token_stride, const float* k_scale, const float* v_scale, void* key_cache,
+    void* value_cache, const uint32_t* block_tables, int32_t block_table_stride,
+    const uint32_t* context_lens, int32_t max_context_len, float softmax_scale, int32_t num_seqs,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int64_t num_blocks, int64_t cache_block_stride, int64_t cache_head_stride, int32_t dtype,
+    int32_t cache_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * paged_attention_noalloc — vpa_paged_attention with no workspace argument
  * and no allocation of any kind. No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture

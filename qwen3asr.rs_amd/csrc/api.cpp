@@ -254,7 +254,8 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
                          int32_t block_size, int64_t num_blocks, int64_t cache_block_stride,
                          int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
                          void* workspace, size_t workspace_bytes, void* stream, bool planned,
-                         const DecodeScratch* scratch, const char* op) {
+                         const DecodeScratch* scratch, const char* op,
+                         const DecodeAppend* append) {
   clear_error();
   if (alibi_slopes != nullptr)
     return fail(VPA_ERR_UNSUPPORTED, "%s: alibi_slopes are not supported", op);
@@ -322,6 +323,20 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
     return fail(VPA_ERR_INVALID_ARGUMENT,
                 "%s: block_table_stride=%d too small for max_context_len=%d (block_size=%d)", op,
                 block_table_stride, max_context_len, block_size);
+  if (append != nullptr) {
+    if (append->key == nullptr || append->value == nullptr)
+      return fail(VPA_ERR_INVALID_ARGUMENT, "%s: key and value must be non-null", op);
+    const int64_t row = (int64_t)num_kv_heads * head_dim;
+    if (append->key_token_stride < row || append->value_token_stride < row)
+      return fail(VPA_ERR_INVALID_ARGUMENT,
+                  "%s: token stride (key=%lld value=%lld) smaller than num_kv_heads*head_dim=%lld",
+                  op, (long long)append->key_token_stride, (long long)append->value_token_stride,
+                  (long long)row);
+    const int eb = dtype_bytes(dtype);
+    if (!aligned16(append->key) || !aligned16(append->value) ||
+        (append->key_token_stride * eb) % 16 != 0 || (append->value_token_stride * eb) % 16 != 0)
+      return fail(VPA_ERR_INVALID_ARGUMENT, "%s: key/value rows must be 16-byte aligned", op);
+  }
   const int part_tokens =
       scratch != nullptr ? decode_part_tokens(dtype, head_dim) : kDecodeMinPartitionTokens;
   const size_t need =
@@ -353,11 +368,36 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
   DecodeWorkspace ws = carve_decode_workspace(workspace, num_seqs, num_heads, head_dim,
                                               max_context_len, part_tokens);
   ws.planned = planned;
+  // The append runs inside the decode launch (the rows kernel's fused form,
+  // 16-bit caches) for small batches only: measured on c3's length rule over
+  // 28 layers (us per step, two launches against one), batch 1: 226 / 152,
+  // 8: 651 / 571, 32: 953 / 889, 64: 1425-1459 / 1459, 128: 2437 / 2524,
+  // 256: 4484 / 4721. Inside a bandwidth-bound decode the token's sector
+  // writes interleave with the tile reads and cost more than the append's
+  // own launch; with few sequences that launch is what costs. Larger batches
+  // and the other configurations run the append kernel on the derived slots,
+  // then the decode: the same bytes and results either way.
+  const bool fuse = append != nullptr &&
+                    decode_fuses_append(dtype, cache_dtype, head_dim, block_size, num_seqs);
+  if (append != nullptr && !fuse) {
+    LastSlots last;
+    last.block_tables = block_tables;
+    last.context_lens = context_lens;
+    last.stride = block_table_stride;
+    last.cap = (int32_t)std::min<int64_t>(max_context_len,
+                                          (int64_t)block_table_stride * block_size);
+    const hipError_t e = launch_append_last_positions(
+        dtype, cache_dtype, append->key, append->value, append->key_token_stride,
+        append->value_token_stride, const_cast<void*>(key_cache), const_cast<void*>(value_cache),
+        last, num_seqs, g, k_scale, v_scale, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_status(op, e);
+  }
   return hip_status(op, launch_paged_decode(dtype, cache_dtype, out, query, key_cache,
                                             value_cache, block_tables, block_table_stride,
                                             context_lens, max_context_len, softmax_scale,
                                             k_scale, v_scale, num_seqs, num_heads, g, ws,
-                                            static_cast<hipStream_t>(stream)));
+                                            static_cast<hipStream_t>(stream),
+                                            fuse ? append : nullptr));
 }
 
 }  // namespace vpa
@@ -399,6 +439,41 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
                               num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
                               cache_head_stride, dtype, cache_dtype, workspace, workspace_bytes,
                               stream, true, nullptr, "paged_attention_planned");
+}
+
+int vpa_reshape_and_cache_paged_attention(
+    void* out, const void* query, const void* key, const void* value, int64_t key_token_stride,
+    int64_t value_token_stride, const float* k_scale, const float* v_scale, void* key_cache,
+    void* value_cache, const uint32_t* block_tables, int32_t block_table_stride,
+    const uint32_t* context_lens, int32_t max_context_len, float softmax_scale, int32_t num_seqs,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int64_t num_blocks, int64_t cache_block_stride, int64_t cache_head_stride, int32_t dtype,
+    int32_t cache_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const DecodeAppend app{key, value, key_token_stride, value_token_stride};
+  return paged_attention_impl(out, query, k_scale, v_scale, key_cache, value_cache, block_tables,
+                              block_table_stride, context_lens, nullptr, max_context_len,
+                              softmax_scale, 1.0f, nullptr, num_seqs, num_heads, num_kv_heads,
+                              head_dim, block_size, num_blocks, cache_block_stride,
+                              cache_head_stride, dtype, cache_dtype, workspace, workspace_bytes,
+                              stream, false, nullptr, "reshape_and_cache_paged_attention", &app);
+}
+
+int vpa_reshape_and_cache_paged_attention_planned(
+    void* out, const void* query, const void* key, const void* value, int64_t key_token_stride,
+    int64_t value_token_stride, const float* k_scale, const float* v_scale, void* key_cache,
+    void* value_cache, const uint32_t* block_tables, int32_t block_table_stride,
+    const uint32_t* context_lens, int32_t max_context_len, float softmax_scale, int32_t num_seqs,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int64_t num_blocks, int64_t cache_block_stride, int64_t cache_head_stride, int32_t dtype,
+    int32_t cache_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const DecodeAppend app{key, value, key_token_stride, value_token_stride};
+  return paged_attention_impl(out, query, k_scale, v_scale, key_cache, value_cache, block_tables,
+                              block_table_stride, context_lens, nullptr, max_context_len,
+                              softmax_scale, 1.0f, nullptr, num_seqs, num_heads, num_kv_heads,
+                              head_dim, block_size, num_blocks, cache_block_stride,
+                              cache_head_stride, dtype, cache_dtype, workspace, workspace_bytes,
+                              stream, true, nullptr, "reshape_and_cache_paged_attention_planned",
+                              &app);
 }
 
 int vpa_paged_attention_plan(const uint32_t* context_lens, int32_t max_context_len,

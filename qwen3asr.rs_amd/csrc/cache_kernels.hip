@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
     int64_t value_token_stride, C* __restrict__ key_cache, C* __restrict__ value_cache,
     const int64_t* __restrict__ slot_mapping, int64_t num_tokens, int64_t num_slots,
     int64_t block_stride, int64_t head_stride, const float* __restrict__ k_scale,
-    const float* __restrict__ v_scale, int32_t num_kv_heads) {
+    const float* __restrict__ v_scale, int32_t num_kv_heads, LastSlots last) {
   constexpr bool kQuant = !std::is_same_v<T, C>;
   static_assert(!kQuant || std::is_same_v<C, fp8_t>, "a cache type differing from the rows is fp8");
   constexpr int X = pack_x<C>();
@@ -107,7 +107,20 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(
 
   if (tid < BS) {
     const int64_t t = t0 + tid;
-    int64_t s = t < num_tokens ? slot_mapping[t] : -1;
+    int64_t s = -1;
+    if (t < num_tokens) {
+      if (slot_mapping != nullptr) {
+        s = slot_mapping[t];
+      } else {
+        // row t is sequence t's token at position context_lens[t] - 1 (none
+        // for an empty context or one the table or max_context_len clamps)
+        const uint32_t L = last.context_lens[t];
+        if (L >= 1u && L <= (uint32_t)last.cap) {
+          const uint32_t pos = L - 1u;
+          s = (int64_t)last.block_tables[t * (int64_t)last.stride + pos / BS] * BS + pos % BS;
+        }
+      }
+    }
     if (s >= num_slots) s = -1;  // out-of-range slots are skipped like padding
     slots[tid] = s;
   }
@@ -436,8 +449,9 @@ hipError_t launch_gather_fp8(void* ok, void* ov, const void* kc, const void* vc,
 
 template <typename T, typename C, int D, int BS>
 hipError_t launch_rc_t(const void* key, const void* value, int64_t kts, int64_t vts, void* kc,
-                       void* vc, const int64_t* slots, int64_t num_tokens, const CacheGeom& g,
-                       const float* k_scale, const float* v_scale, hipStream_t stream) {
+                       void* vc, const int64_t* slots, const LastSlots& last,
+                       int64_t num_tokens, const CacheGeom& g, const float* k_scale,
+                       const float* v_scale, hipStream_t stream) {
   const int64_t groups = (num_tokens + BS - 1) / BS;
 #if VPA_APPEND_HEAD_FAST
   dim3 grid((unsigned)(groups * g.num_kv_heads));
@@ -448,18 +462,19 @@ hipError_t launch_rc_t(const void* key, const void* value, int64_t kts, int64_t 
                      static_cast<const T*>(key), static_cast<const T*>(value), kts, vts,
                      static_cast<C*>(kc), static_cast<C*>(vc), slots, num_tokens,
                      g.num_blocks * (int64_t)BS, g.block_stride, g.head_stride, k_scale, v_scale,
-                     (int32_t)g.num_kv_heads);
+                     (int32_t)g.num_kv_heads, last);
   return hipGetLastError();
 }
 template <typename T, int D, int BS>
 hipError_t launch_rc(const void* key, const void* value, int64_t kts, int64_t vts, void* kc,
-                     void* vc, const int64_t* slots, int64_t num_tokens, const CacheGeom& g,
-                     const float* k_scale, const float* v_scale, bool fp8, hipStream_t stream) {
+                     void* vc, const int64_t* slots, LastSlots last, int64_t num_tokens,
+                     const CacheGeom& g, const float* k_scale, const float* v_scale, bool fp8,
+                     hipStream_t stream) {
   if (fp8)
-    return launch_rc_t<T, fp8_t, D, BS>(key, value, kts, vts, kc, vc, slots, num_tokens, g,
-                                        k_scale, v_scale, stream);
-  return launch_rc_t<T, T, D, BS>(key, value, kts, vts, kc, vc, slots, num_tokens, g, k_scale,
-                                  v_scale, stream);
+    return launch_rc_t<T, fp8_t, D, BS>(key, value, kts, vts, kc, vc, slots, last, num_tokens,
+                                        g, k_scale, v_scale, stream);
+  return launch_rc_t<T, T, D, BS>(key, value, kts, vts, kc, vc, slots, last, num_tokens, g,
+                                  k_scale, v_scale, stream);
 }
 
 template <typename T, int D, int BS>
@@ -542,8 +557,21 @@ hipError_t launch_reshape_and_cache(int dtype, int cache_dtype, const void* key,
                                     int64_t num_tokens, const CacheGeom& g, const float* k_scale,
                                     const float* v_scale, hipStream_t stream) {
   return dispatch_rc(dtype, g.head_dim, g.block_size, key, value, key_token_stride,
-                     value_token_stride, key_cache, value_cache, slot_mapping, num_tokens, g,
-                     k_scale, v_scale, cache_dtype == VPA_DTYPE_FP8_E4M3, stream);
+                     value_token_stride, key_cache, value_cache, slot_mapping, LastSlots{},
+                     num_tokens, g, k_scale, v_scale, cache_dtype == VPA_DTYPE_FP8_E4M3, stream);
+}
+
+hipError_t launch_append_last_positions(int dtype, int cache_dtype, const void* key,
+                                        const void* value, int64_t key_token_stride,
+                                        int64_t value_token_stride, void* key_cache,
+                                        void* value_cache, const LastSlots& last,
+                                        int32_t num_seqs, const CacheGeom& g,
+                                        const float* k_scale, const float* v_scale,
+                                        hipStream_t stream) {
+  return dispatch_rc(dtype, g.head_dim, g.block_size, key, value, key_token_stride,
+                     value_token_stride, key_cache, value_cache,
+                     static_cast<const int64_t*>(nullptr), last, (int64_t)num_seqs, g, k_scale,
+                     v_scale, cache_dtype == VPA_DTYPE_FP8_E4M3, stream);
 }
 
 hipError_t launch_gather_kv_cache(int cache_dtype, int out_dtype, void* out_key,

@@ -53,6 +53,31 @@ __device__ __forceinline__ uint4 tile_load(const uint4* p) {
   if constexpr (VPA_DECODE_STREAM_LOADS) return load_stream(p);
   else return *p;
 }
+// Workgroup barrier for data exchanged through LDS: waits for this wave's LDS
+// operations only (outstanding global loads and stores stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// v with its 16-bit element e (0..7; uniform) replaced by val, without a
+// runtime-indexed array
+__device__ __forceinline__ uint4 put_u16(uint4 v, int e, uint32_t val) {
+  const uint32_t sh = (uint32_t)(e & 1) * 16u;
+  const uint32_t keep = ~(0xffffu << sh), ins = (val & 0xffffu) << sh;
+  const int w = e >> 1;
+  v.x = w == 0 ? (v.x & keep) | ins : v.x;
+  v.y = w == 1 ? (v.y & keep) | ins : v.y;
+  v.z = w == 2 ? (v.z & keep) | ins : v.z;
+  v.w = w == 3 ? (v.w & keep) | ins : v.w;
+  return v;
+}
+// 16-byte non-temporal store (the fused append's whole sectors)
+__device__ __forceinline__ void tile_store(uint4* p, const uint4& v) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
+}
 
 template <typename T, int D, int BS, int G>
 __global__ __launch_bounds__(64) void paged_decode_kernel(
@@ -470,7 +495,18 @@ constexpr int rows_waves_per_eu() {
   return qvec >= 16 ? 2 : f8 ? VPA_DECODE_FP8_WAVES_PER_EU : VPA_DECODE_ROWS_WAVES_PER_EU;
 }
 
-template <typename T, typename C, int D, int BS, int G, int PT, int NW>
+// kAppend (16-bit caches): the launch also appends each sequence's new K/V
+// row (new_key / new_value, one token per sequence) at position L - 1 of its
+// context, the slot vASR's decode metadata gives the step's token
+// (paged_kv_cache.rs:985-1017), in place of a reshape_and_cache launch before
+// it. The wave whose partition ends at the context's last block holds that
+// block's K and V tiles in registers anyway: it stages the two new rows in
+// LDS at its start, puts the token's values into the tiles before using
+// them, and writes back whole 32-byte sectors with non-temporal stores: the
+// 16 key units of the token with their neighbours (tokens 2i, 2i + 1 share a
+// sector), and the whole value tile (every 32-byte value row holds the
+// token). No partially written sector reaches HBM.
+template <typename T, typename C, int D, int BS, int G, int PT, int NW, bool kAppend = false>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(rows_waves_per_eu<C, D, BS, G>())))
 void paged_decode_rows_kernel(
@@ -480,9 +516,11 @@ void paged_decode_rows_kernel(
     int64_t num_blocks, int64_t block_stride, int64_t head_stride, float* __restrict__ part_out,
     int32_t max_parts, const uint2* __restrict__ items, const uint32_t* __restrict__ queue,
     int32_t num_seqs, int32_t max_ctx, int32_t cap_tokens, const float* __restrict__ k_scale,
-    const float* __restrict__ v_scale) {
+    const float* __restrict__ v_scale, const T* __restrict__ new_key,
+    const T* __restrict__ new_value, int64_t new_key_stride, int64_t new_value_stride) {
   constexpr bool kF8 = std::is_same_v<C, fp8_t>;
   static_assert(kF8 || std::is_same_v<C, T>, "cache type is the query type or fp8");
+  static_assert(!(kAppend && kF8), "the fused append writes 16-bit caches");
   constexpr int X = pack_x<C>();
   static_assert(X == (kF8 ? 16 : 8), "16-bit or fp8 cache elements only");
   constexpr int PB = PT / BS;        // blocks per wave partition
@@ -517,6 +555,8 @@ void paged_decode_rows_kernel(
   __shared__ float s_logit[NW][G][PT];
   __shared__ __align__(16) uint16_t s_p[NW][G][PT];
   __shared__ float s_m[NW][G], s_l[NW][G];
+  constexpr int NR = D / 8;  // 16-byte vectors of a new 16-bit K (or V) row
+  __shared__ __align__(16) uint4 s_new[kAppend ? 2 * NR : 1];
 
   const int lane = threadIdx.x & 63;
   // Uniform where a stage holds at most two tiles: the partition bounds,
@@ -560,6 +600,11 @@ void paged_decode_rows_kernel(
   const int c_nb = min(PB * NW, nblk - c_begin);
   const int b_begin = c_begin + (c_nb * wave) / NW;
   const int nb = c_begin + (c_nb * (wave + 1)) / NW - b_begin;  // 0: idle wave
+  // fused append: this wave's partition ends at the context's last block,
+  // which holds the new token at offset app_off (a context clamped by
+  // max_context_len or the table appends nothing)
+  const bool app = kAppend && nb > 0 && b_begin + nb == nblk && item.y == (uint32_t)L;
+  const int app_off = (L - 1) % BS;
 
   float acc[G][NACC];
   float m[G], lsum[G];
@@ -598,6 +643,15 @@ void paged_decode_rows_kernel(
               *reinterpret_cast<const uint4*>(qrow + (lane / BS + k * LPT) * X + 8 * h2);
     }
 
+    // the new K and V rows of head j (the appending wave's lanes 0 .. 2 NR - 1),
+    // loaded before the first tiles so that the wait for those covers them
+    uint4 nrow = make_uint4(0u, 0u, 0u, 0u);
+    if (kAppend && app && lane < 2 * NR)
+      nrow = *reinterpret_cast<const uint4*>(
+          lane < NR ? new_key + (int64_t)s * new_key_stride + (int64_t)j * D + lane * 8
+                    : new_value + (int64_t)s * new_value_stride + (int64_t)j * D +
+                          (lane - NR) * 8);
+
     const int64_t head_off = (int64_t)j * head_stride;
     const uint4* kbase = reinterpret_cast<const uint4*>(key_cache + head_off);
     const uint4* vbase = reinterpret_cast<const uint4*>(value_cache + head_off);
@@ -634,9 +688,27 @@ void paged_decode_rows_kernel(
 #pragma unroll
       for (int u = 0; u < BKS; ++u) {
         bool ok;
-        tile_block(st, u, ok);
+        const uint32_t phys = tile_block(st, u, ok);
         const int bi = st * BKS + u;
         const bool valid = ok && (b_begin + bi) * BS + t < L;
+        uint4 kt[KPL];
+#pragma unroll
+        for (int k = 0; k < KPL; ++k) kt[k] = buf[u * KPL + k];
+        if constexpr (kAppend) {
+          if (app && ok && bi == nb - 1) {  // (uniform) the new token's block
+            // lane l holds chunk l / BS + k LPT of token t: the token's
+            // lanes take the new row's chunks, then the lanes of its 32-byte
+            // sectors write them back whole
+            if (t == app_off)
+#pragma unroll
+              for (int k = 0; k < KPL; ++k) kt[k] = s_new[lane / BS + k * LPT];
+            if ((t >> 1) == (app_off >> 1)) {
+              uint4* dst = const_cast<uint4*>(kbase) + (int64_t)phys * bstride_v + lane;
+#pragma unroll
+              for (int k = 0; k < KPL; ++k) tile_store(dst + 64 * k, kt[k]);
+            }
+          }
+        }
         float qk[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) qk[g] = 0.f;
@@ -644,13 +716,13 @@ void paged_decode_rows_kernel(
         for (int k = 0; k < KPL; ++k) {
           if constexpr (kF8) {
             uint4 klo, khi;
-            fp8x16_to_pk<T>(buf[u * KPL + k], klo, khi);
+            fp8x16_to_pk<T>(kt[k], klo, khi);
 #pragma unroll
             for (int g = 0; g < G; ++g)
               qk[g] = dot16<T>(qv[g][k][1], khi, dot16<T>(qv[g][k][0], klo, qk[g]));
           } else {
 #pragma unroll
-            for (int g = 0; g < G; ++g) qk[g] = dot16<T>(qv[g][k][0], buf[u * KPL + k], qk[g]);
+            for (int g = 0; g < G; ++g) qk[g] = dot16<T>(qv[g][k][0], kt[k], qk[g]);
           }
         }
 #pragma unroll
@@ -665,12 +737,28 @@ void paged_decode_rows_kernel(
 #pragma unroll
       for (int u = 0; u < BKS; ++u) {
         bool ok;
-        tile_block(st, u, ok);
+        const uint32_t phys = tile_block(st, u, ok);
         if (!ok) continue;
         const int bi = st * BKS + u;
         uint4 vv[NVV];
 #pragma unroll
         for (int k = 0; k < NVV; ++k) vv[k] = buf[u * KPL + k];
+        if constexpr (kAppend) {
+          if (app && bi == nb - 1) {  // (uniform) the new token's block
+            // lane l holds rows l / VPR + k DSTEP, tokens seg X .. seg X + X - 1:
+            // the lanes of the token's segment put in its values, then the
+            // whole tile is written back
+            if (seg == app_off / X) {
+              const uint16_t* nv = reinterpret_cast<const uint16_t*>(&s_new[NR]);
+#pragma unroll
+              for (int k = 0; k < NVV; ++k)
+                vv[k] = put_u16(vv[k], app_off % X, nv[lane / VPR + k * DSTEP]);
+            }
+            uint4* dst = const_cast<uint4*>(vbase) + (int64_t)phys * bstride_v + lane;
+#pragma unroll
+            for (int k = 0; k < NVV; ++k) tile_store(dst + 64 * k, vv[k]);
+          }
+        }
         if constexpr (kPairRows) {
           // vector k of lane l: rows 2 (l + 64 k) and 2 (l + 64 k) + 1, the
           // block's 8 tokens each, against the block's 8 probabilities
@@ -760,6 +848,10 @@ void paged_decode_rows_kernel(
     uint4 bufA[NV], bufB[NV];
     load_stage(kbase, 0, bufA);
     load_stage(kbase, 1, bufB);
+    if (kAppend && app) {
+      if (lane < 2 * NR) s_new[lane] = nrow;
+      lds_wave_sync();
+    }
     for (int st = 0; st + 2 < nks; st += 2) {
       compute_k(st, bufA);
       load_stage(kbase, st + 2, bufA);
@@ -825,7 +917,10 @@ void paged_decode_rows_kernel(
   // ---- merge the NW partitions of the chunk in LDS ----
   // Each wave leaves its unnormalised output (in its own s_logit slot, free
   // after the softmax) and its max / sum; then the workgroup combines them.
-  __syncthreads();
+  // The barriers wait for LDS only: __syncthreads() would also wait for this
+  // wave's outstanding global stores (the fused append's sector writes),
+  // which nothing here reads.
+  lds_barrier();
   {
     float* my_row = &s_logit[wave][0][0];
     if constexpr (kPairRows) {
@@ -850,7 +945,7 @@ void paged_decode_rows_kernel(
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   // thread e of the workgroup combines output elements e, e + 64*NW, ...
   // (contiguous per head row, so stores write whole lines)
   const bool single = nchunks == 1;
@@ -1010,12 +1105,18 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   }
 }
 
+// Shapes whose rows kernel takes the fused append: at least 2 KiB of 16-bit
+// (block, head) tile, i.e. at most two tiles per 8-load stage (more tiles per
+// stage spill scalar registers with the append's extra state).
+constexpr bool fused_append_shape(int d, int bs) { return d * bs >= 2048; }
+
 template <typename T, typename C, int D, int BS, int G>
 hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const void* vc,
                                 const uint32_t* bt, int32_t bts, const uint32_t* cl,
                                 int32_t max_ctx, float scale, int32_t num_seqs,
                                 int32_t num_heads, const CacheGeom& g, const DecodeWorkspace& ws,
-                                hipStream_t stream, const float* k_scale, const float* v_scale) {
+                                hipStream_t stream, const float* k_scale, const float* v_scale,
+                                const DecodeAppend* app) {
   constexpr bool kFp8 = std::is_same_v<C, fp8_t>;
   constexpr int PT = kFp8 ? kF8PT : kRowsPT;
   constexpr int NW = kFp8 ? kF8Waves : kRowsWaves;
@@ -1031,12 +1132,29 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
   }
   const int max_chunks = max(1, (max_ctx + kChunk - 1) / kChunk);
   const int64_t units = (int64_t)num_seqs * max_chunks * g.num_kv_heads;
-  hipLaunchKernelGGL((paged_decode_rows_kernel<T, C, D, BS, G, PT, NW>),
-                     dim3((unsigned)units), dim3(64 * NW), 0, stream,
-                     static_cast<T*>(out), static_cast<const T*>(q), static_cast<const C*>(kc),
-                     static_cast<const C*>(vc), bt, bts, scale, num_heads, g.num_kv_heads,
-                     g.num_blocks, g.block_stride, g.head_stride, ws.part_out, ws.max_parts,
-                     ws.items, ws.queue, num_seqs, max_ctx, cap_tokens, k_scale, v_scale);
+  if constexpr (!kFp8 && fused_append_shape(D, BS)) {
+    if (app != nullptr) {
+      hipLaunchKernelGGL((paged_decode_rows_kernel<T, C, D, BS, G, PT, NW, true>),
+                         dim3((unsigned)units), dim3(64 * NW), 0, stream, static_cast<T*>(out),
+                         static_cast<const T*>(q), static_cast<const C*>(kc),
+                         static_cast<const C*>(vc), bt, bts, scale, num_heads, g.num_kv_heads,
+                         g.num_blocks, g.block_stride, g.head_stride, ws.part_out,
+                         ws.max_parts, ws.items, ws.queue, num_seqs, max_ctx, cap_tokens,
+                         k_scale, v_scale, static_cast<const T*>(app->key),
+                         static_cast<const T*>(app->value), app->key_token_stride,
+                         app->value_token_stride);
+    }
+  }
+  if (kFp8 || !fused_append_shape(D, BS) || app == nullptr) {
+    hipLaunchKernelGGL((paged_decode_rows_kernel<T, C, D, BS, G, PT, NW>),
+                       dim3((unsigned)units), dim3(64 * NW), 0, stream, static_cast<T*>(out),
+                       static_cast<const T*>(q), static_cast<const C*>(kc),
+                       static_cast<const C*>(vc), bt, bts, scale, num_heads, g.num_kv_heads,
+                       g.num_blocks, g.block_stride, g.head_stride, ws.part_out, ws.max_parts,
+                       ws.items, ws.queue, num_seqs, max_ctx, cap_tokens, k_scale, v_scale,
+                       static_cast<const T*>(nullptr), static_cast<const T*>(nullptr),
+                       (int64_t)0, (int64_t)0);
+  }
   e = hipGetLastError();
   if (e != hipSuccess || max_chunks <= 1) return e;
   const int64_t munits = (int64_t)num_seqs * num_heads;
@@ -1053,10 +1171,11 @@ hipError_t launch_decode_rows(void* out, const void* q, const void* kc, const vo
                               const uint32_t* bt, int32_t bts, const uint32_t* cl,
                               int32_t max_ctx, float scale, int32_t num_seqs, int32_t num_heads,
                               const CacheGeom& g, const DecodeWorkspace& ws, hipStream_t stream,
-                              const float* k_scale, const float* v_scale) {
+                              const float* k_scale, const float* v_scale,
+                              const DecodeAppend* app) {
   return launch_decode_rows_c<T, T, D, BS, G>(out, q, kc, vc, bt, bts, cl, max_ctx, scale,
                                               num_seqs, num_heads, g, ws, stream, k_scale,
-                                              v_scale);
+                                              v_scale, app);
 }
 template <typename T, int D, int BS, int G>
 hipError_t launch_decode_rows_fp8(void* out, const void* q, const void* kc, const void* vc,
@@ -1064,10 +1183,11 @@ hipError_t launch_decode_rows_fp8(void* out, const void* q, const void* kc, cons
                                   int32_t max_ctx, float scale, int32_t num_seqs,
                                   int32_t num_heads, const CacheGeom& g,
                                   const DecodeWorkspace& ws, hipStream_t stream,
-                                  const float* k_scale, const float* v_scale) {
+                                  const float* k_scale, const float* v_scale,
+                                  const DecodeAppend*) {
   return launch_decode_rows_c<T, fp8_t, D, BS, G>(out, q, kc, vc, bt, bts, cl, max_ctx, scale,
                                                   num_seqs, num_heads, g, ws, stream, k_scale,
-                                                  v_scale);
+                                                  v_scale, nullptr);
 }
 
 template <typename T, int D, int BS, int G>
@@ -1075,7 +1195,7 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
                            const uint32_t* bt, int32_t bts, const uint32_t* cl, int32_t max_ctx,
                            float scale, int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
                            const DecodeWorkspace& ws, hipStream_t stream, const float*,
-                           const float*) {
+                           const float*, const DecodeAppend*) {
   const int max_parts = (max_ctx + kPT - 1) / kPT;
   dim3 grid((unsigned)g.num_kv_heads, (unsigned)num_seqs, (unsigned)(max_parts > 0 ? max_parts : 1));
   hipLaunchKernelGGL((paged_decode_kernel<T, D, BS, G>), grid, dim3(64), 0, stream,
@@ -1307,6 +1427,12 @@ bool decode_supported(int dtype, int head_dim, int block_size, int group) {
          (head_dim * block_size / x) % 64 == 0 && (group == 1 || group == 2 || group == 4);
 }
 
+bool decode_fuses_append(int dtype, int cache_dtype, int head_dim, int block_size,
+                         int num_seqs) {
+  return cache_dtype == dtype && decode_uses_rows_kernel(dtype, head_dim) &&
+         fused_append_shape(head_dim, block_size) && num_seqs <= kFusedAppendMaxSeqs;
+}
+
 bool decode_uses_rows_kernel(int dtype, int head_dim) {
   return (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) &&
          (head_dim == 64 || head_dim == 128);
@@ -1376,17 +1502,18 @@ hipError_t launch_paged_decode(int dtype, int cache_dtype, void* out, const void
                                const uint32_t* context_lens, int32_t max_context_len,
                                float scale, const float* k_scale, const float* v_scale,
                                int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
-                               const DecodeWorkspace& ws, hipStream_t stream) {
+                               const DecodeWorkspace& ws, hipStream_t stream,
+                               const DecodeAppend* append) {
   const int group = num_heads / g.num_kv_heads;
   if (cache_dtype == VPA_DTYPE_FP8_E4M3)
     return dispatch_decode_fp8(dtype, g.head_dim, g.block_size, group, out, query, key_cache,
                                value_cache, block_tables, block_table_stride, context_lens,
                                max_context_len, scale, num_seqs, num_heads, g, ws, stream,
-                               k_scale, v_scale);
+                               k_scale, v_scale, append);
   return dispatch_decode(dtype, g.head_dim, g.block_size, group, out, query, key_cache,
                          value_cache, block_tables, block_table_stride, context_lens,
                          max_context_len, scale, num_seqs, num_heads, g, ws, stream, k_scale,
-                         v_scale);
+                         v_scale, append);
 }
 
 }  // namespace vpa

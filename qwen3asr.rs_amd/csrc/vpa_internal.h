@@ -45,6 +45,25 @@ struct DecodeWorkspace {
   bool planned = false;  // the work list is already in the workspace (skip the plan launch)
 };
 
+// New K/V rows of a decode step appended by the decode launch itself
+// (vpa_reshape_and_cache_paged_attention): row s (one token, num_kv_heads *
+// head_dim elements of the cache type) goes to position context_lens[s] - 1
+// of sequence s's block table.
+struct DecodeAppend {
+  const void* key;
+  const void* value;
+  int64_t key_token_stride;
+  int64_t value_token_stride;
+};
+
+// Largest batch whose decode append runs inside the decode launch.
+constexpr int kFusedAppendMaxSeqs = 48;
+// True when vpa_reshape_and_cache_paged_attention runs its append inside the
+// decode launch (16-bit cache of the query's type, head_dim 64 / 128 with a
+// (block, head) tile of at least 2 KiB, at most kFusedAppendMaxSeqs sequences).
+bool decode_fuses_append(int dtype, int cache_dtype, int head_dim, int block_size,
+                         int num_seqs);
+
 // Compute units of the current device (cached per device).
 int device_cu_count();
 
@@ -77,7 +96,8 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
                          int64_t num_blocks, int64_t cache_block_stride,
                          int64_t cache_head_stride, int32_t dtype, int32_t cache_dtype,
                          void* workspace, size_t workspace_bytes, void* stream, bool planned,
-                         const DecodeScratch* scratch, const char* op);
+                         const DecodeScratch* scratch, const char* op,
+                         const DecodeAppend* append = nullptr);
 
 // Split-K partition (tokens) of the decode kernel that runs for a query
 // dtype and head_dim: the rows kernel's chunk, or the generic kernel's
@@ -104,6 +124,24 @@ hipError_t launch_reshape_and_cache(int dtype, int cache_dtype, const void* key,
                                     int64_t num_tokens, const CacheGeom& g, const float* k_scale,
                                     const float* v_scale, hipStream_t stream);
 
+// The slot of row t of an append derived from the decode metadata: position
+// context_lens[t] - 1 of block-table row t (no slot for an empty context or
+// one above cap = min(max_context_len, block_table_stride * block_size)).
+struct LastSlots {
+  const uint32_t* block_tables = nullptr;
+  const uint32_t* context_lens = nullptr;
+  int32_t stride = 0;
+  int32_t cap = 0;
+};
+// reshape_and_cache of num_seqs rows, row s at sequence s's last position.
+hipError_t launch_append_last_positions(int dtype, int cache_dtype, const void* key,
+                                        const void* value, int64_t key_token_stride,
+                                        int64_t value_token_stride, void* key_cache,
+                                        void* value_cache, const LastSlots& last,
+                                        int32_t num_seqs, const CacheGeom& g,
+                                        const float* k_scale, const float* v_scale,
+                                        hipStream_t stream);
+
 // out_dtype is cache_dtype (copy) or, for an fp8 cache, f32 / f16 / bf16
 // (dequantised with *k_scale / *v_scale).
 hipError_t launch_gather_kv_cache(int cache_dtype, int out_dtype, void* out_key,
@@ -121,7 +159,8 @@ hipError_t launch_paged_decode(int dtype, int cache_dtype, void* out, const void
                                const uint32_t* context_lens, int32_t max_context_len,
                                float scale, const float* k_scale, const float* v_scale,
                                int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
-                               const DecodeWorkspace& ws, hipStream_t stream);
+                               const DecodeWorkspace& ws, hipStream_t stream,
+                               const DecodeAppend* append = nullptr);
 
 hipError_t launch_prefill_paged(int dtype, int cache_dtype, void* out, const void* query,
                                 const void* key_cache, const void* value_cache,

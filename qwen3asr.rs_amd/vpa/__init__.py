@@ -18,6 +18,7 @@ from .ops import (  # noqa: F401
     paged_attention_varlen_prefill,
     paged_attention_workspace,
     reshape_and_cache,
+    reshape_and_cache_paged_attention,
 )
 from .graph import DecodeGraphCache  # noqa: F401
 from .step import DeviceDecodeStep  # noqa: F401
@@ -37,4 +38,5 @@ __all__ = [
     "paged_attention_varlen_prefill",
     "paged_attention_workspace",
     "reshape_and_cache",
+    "reshape_and_cache_paged_attention",
 ]

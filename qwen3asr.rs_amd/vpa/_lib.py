@@ -52,6 +52,12 @@ SIGNATURES = {
     "vpa_paged_attention_planned": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32,
                                                    _f32, _f32, _p, _i32, _i32, _i32, _i32, _i32,
                                                    _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),
+    "vpa_reshape_and_cache_paged_attention": (ctypes.c_int, [
+        _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32, _p, _i32, _f32, _i32, _i32, _i32,
+        _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),
+    "vpa_reshape_and_cache_paged_attention_planned": (ctypes.c_int, [
+        _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32, _p, _i32, _f32, _i32, _i32, _i32,
+        _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),
     "vpa_paged_attention_noalloc": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32,
                                                    _f32, _f32, _p, _i32, _i32, _i32, _i32, _i32,
                                                    _i64, _i64, _i64, _i32, _i32, _p]),

@@ -196,6 +196,66 @@ def paged_attention(q: torch.Tensor, k_scale: Optional[torch.Tensor],
     return out
 
 
+def reshape_and_cache_paged_attention(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                      k_scale: Optional[torch.Tensor],
+                                      v_scale: Optional[torch.Tensor], key_cache: torch.Tensor,
+                                      value_cache: torch.Tensor, block_tables: torch.Tensor,
+                                      context_lens: torch.Tensor, max_context_len: int,
+                                      softmax_scale: float, *, out: Optional[torch.Tensor] = None,
+                                      workspace: Optional[torch.Tensor] = None,
+                                      planned: bool = False) -> torch.Tensor:
+    """``reshape_and_cache`` of one new K/V row per sequence ([B, KVH, D], the
+    query's dtype) at position ``context_lens[s] - 1`` of its block table,
+    then ``paged_attention`` over the caches, behind one call (one launch for
+    small batches over 16-bit caches); returns [B, H, D]. Equal to the two
+    calls with that slot mapping as long as no two sequences' last positions
+    share a block."""
+    _require_device(q, key, value, key_cache, value_cache, block_tables, context_lens)
+    nb, kvh, d, bs, bstride, hstride = cache_geometry(key_cache, value_cache)
+    if q.dim() != 3 or q.shape[2] != d:
+        raise _err(f"q must be [B, H, {d}], got {tuple(q.shape)}")
+    b, h, _ = q.shape
+    if key.shape != (b, kvh, d) or value.shape != key.shape:
+        raise _err(f"key/value must be [{b}, {kvh}, {d}], got {tuple(key.shape)} and "
+                   f"{tuple(value.shape)}")
+    if key.dtype != q.dtype or value.dtype != q.dtype:
+        raise _err(f"key/value dtype must be the query's {q.dtype}")
+    if block_tables.dtype != torch.uint32 or block_tables.dim() != 2 or block_tables.shape[0] != b:
+        raise _err(f"block_tables must be u32 [{b}, cols], got {block_tables.dtype} "
+                   f"{tuple(block_tables.shape)}")
+    if context_lens.dtype != torch.uint32 or context_lens.shape != (b,):
+        raise _err(f"context_lens must be u32 [{b}], got {context_lens.dtype} "
+                   f"{tuple(context_lens.shape)}")
+    if key.stride(2) != 1 or key.stride(1) != d:
+        key = key.contiguous()
+    if value.stride(2) != 1 or value.stride(1) != d:
+        value = value.contiguous()
+    q = q.contiguous()
+    block_tables = block_tables.contiguous()
+    context_lens = context_lens.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise _err("out must be a contiguous tensor shaped and typed like q")
+    lib = _lib.load()
+    need = lib.vpa_paged_attention_workspace_size(b, h, d, int(max_context_len))
+    if workspace is None and need > 0:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if planned and workspace is None:
+        raise _err("planned=True needs the workspace paged_attention_plan filled")
+    fn = (lib.vpa_reshape_and_cache_paged_attention_planned if planned
+          else lib.vpa_reshape_and_cache_paged_attention)
+    check(fn(
+        out.data_ptr(), q.data_ptr(), key.data_ptr(), value.data_ptr(), key.stride(0),
+        value.stride(0), _ptr(k_scale), _ptr(v_scale), key_cache.data_ptr(),
+        value_cache.data_ptr(), block_tables.data_ptr(), block_tables.shape[1],
+        context_lens.data_ptr(), int(max_context_len), float(softmax_scale), b, h, kvh, d, bs, nb,
+        bstride, hstride, dtype_code(q.dtype), dtype_code(key_cache.dtype), _ptr(workspace),
+        ws_bytes, _stream(q)))
+    return out
+
+
 def paged_attention_plan(context_lens: torch.Tensor, max_context_len: int,
                          block_table_stride: int, num_heads: int, key_cache: torch.Tensor,
                          value_cache: torch.Tensor, dtype: torch.dtype,

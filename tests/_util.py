@@ -84,3 +84,35 @@ def assert_attention_close(got_f32: np.ndarray, want_f64: np.ndarray, code: int,
     worst = np.max(err / bound) if err.size else 0.0
     assert worst <= 1.0, (f"{what}: max err {err.max():.3e} exceeds tol {tol} "
                           f"(ratio {worst:.2f}, max|ref| {scale:.3e})")
+
+
+def attention_errors(got_f32: np.ndarray, want_f64: np.ndarray, code: int):
+    """(worst element / element-wise bound of assert_attention_close, worst
+    per-row normwise relative error); a row is one output vector along the
+    last axis (head_dim)."""
+    tol = TOL[code]
+    want = want_f64.astype(np.float64)
+    got = got_f32.astype(np.float64)
+    scale = np.abs(want).max() if want.size else 0.0
+    err = np.abs(got - want)
+    bound = tol * (np.abs(want) + FLOOR[code] * scale) + 1e-30
+    worst = float(np.max(err / bound)) if err.size else 0.0
+    num = np.sqrt(((got - want) ** 2).sum(axis=-1))
+    den = np.sqrt((want ** 2).sum(axis=-1)) + 1e-300
+    return worst, float(np.max(num / den)) if num.size else 0.0
+
+
+def assert_attention_close_normwise(got_f32: np.ndarray, want_f64: np.ndarray, code: int,
+                                    what=""):
+    """||got - want||_2 <= tol * ||want||_2 for every output row (one
+    (sequence, head) vector of head_dim values), at the stated tolerance
+    (TOL): the acceptance bar read normwise, for the regions where single
+    elements near zero sit at the rounding of their cancelling terms."""
+    tol = TOL[code]
+    want = want_f64.astype(np.float64)
+    got = got_f32.astype(np.float64)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    num = np.sqrt(((got - want) ** 2).sum(axis=-1))
+    den = np.sqrt((want ** 2).sum(axis=-1))
+    worst = float(np.max(num / np.maximum(den, 1e-300))) if num.size else 0.0
+    assert worst <= tol, f"{what}: normwise rel err {worst:.3e} exceeds tol {tol}"

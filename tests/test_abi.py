@@ -419,3 +419,52 @@ def test_noalloc_validates_before_touching_the_device():
                                          100, 8 * 128 * 16, 128 * 16, _lib.DTYPE_BF16,
                                          _lib.DTYPE_BF16, None)
     assert rc == _lib.VPA_ERR_WORKSPACE and "static scratch" in lib.vpa_last_error().decode()
+
+
+# ---- fused append + decode -------------------------------------------------------
+
+def fused_args(**over):
+    args = dict(out=FAKE, q=FAKE, k=FAKE, v=FAKE, kts=8 * 128, vts=8 * 128, ks=None, vs=None,
+                kc=FAKE, vc=FAKE, bt=FAKE, bts=64, cl=FAKE, max_ctx=1024, scale=0.088, b=4, h=16,
+                kvh=8, d=128, bs=16, nb=100, bstride=8 * 128 * 16, hstride=128 * 16,
+                dtype=_lib.DTYPE_BF16, cdtype=_lib.DTYPE_BF16, ws=None, ws_bytes=0, stream=None)
+    args.update(over)
+    return args
+
+
+def fused_call(**over):
+    lib = _lib.load()
+    rc = lib.vpa_reshape_and_cache_paged_attention(*fused_args(**over).values())
+    return rc, lib.vpa_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,needle", [
+    (dict(k=None), _lib.VPA_ERR_INVALID_ARGUMENT, "key and value"),
+    (dict(vts=100), _lib.VPA_ERR_INVALID_ARGUMENT, "token stride"),
+    (dict(k=FAKE + 2), _lib.VPA_ERR_INVALID_ARGUMENT, "16-byte aligned"),
+    (dict(h=12), _lib.VPA_ERR_INVALID_ARGUMENT, "multiple"),
+    (dict(bts=10), _lib.VPA_ERR_INVALID_ARGUMENT, "block_table_stride"),
+    (dict(cdtype=_lib.DTYPE_FP8_E4M3), _lib.VPA_ERR_INVALID_ARGUMENT, "k_scale"),
+    (dict(dtype=_lib.DTYPE_F32), _lib.VPA_ERR_UNSUPPORTED, "differs"),
+    (dict(ws_bytes=0, max_ctx=4096, bts=256), _lib.VPA_ERR_WORKSPACE, "workspace"),
+])
+def test_fused_append_decode_host_validation(over, code, needle):
+    """vpa_reshape_and_cache_paged_attention: every check of the two calls it
+    stands for runs on the host, with the entry point's name."""
+    rc, msg = fused_call(**over)
+    assert rc == code, msg
+    assert needle in msg, msg
+    assert msg.startswith("reshape_and_cache_paged_attention")
+
+
+def test_fused_append_decode_planned_validates_alike():
+    lib = _lib.load()
+    for over in (dict(dtype=_lib.DTYPE_F32), dict(k=None), dict(h=12), dict(bts=10)):
+        args = fused_args(**over)
+        rc_a = lib.vpa_reshape_and_cache_paged_attention(*args.values())
+        msg_a = lib.vpa_last_error().decode()
+        rc_b = lib.vpa_reshape_and_cache_paged_attention_planned(*args.values())
+        msg_b = lib.vpa_last_error().decode()
+        assert rc_a == rc_b != 0
+        assert msg_b.replace("_planned", "") == msg_a
+    assert fused_call(b=0)[0] == 0

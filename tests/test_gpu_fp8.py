@@ -115,7 +115,8 @@ def test_fp8_gather_every_code_bit_exact(device, out, scales):
         np.testing.assert_array_equal(got[fin], want[fin])
 
 
-def fp8_decode_case(device, code, h, kvh, d, bs, lens, seed, scales=(1.0, 1.0), planned=False):
+def fp8_decode_case(device, code, h, kvh, d, bs, lens, seed, scales=(1.0, 1.0), planned=False,
+                    softmax_scale=None):
     rng = np.random.default_rng(seed)
     ks, vs = scales
     need = sum((int(L) + bs - 1) // bs for L in lens)
@@ -132,7 +133,7 @@ def fp8_decode_case(device, code, h, kvh, d, bs, lens, seed, scales=(1.0, 1.0), 
     q = random_words(rng, (len(lens), h, d), code)
     lens = np.asarray(lens, dtype=np.uint32)
     max_ctx = int(lens.max())
-    scale = d ** -0.5
+    scale = d ** -0.5 if softmax_scale is None else softmax_scale
     args = (to_dev(q, code, device), scalar(ks, device), scalar(vs, device), f8(kc, device),
             f8(vc, device), u32(bt, device), u32(lens, device), None, max_ctx, scale, 1.0, None)
     if planned:
@@ -163,6 +164,17 @@ def test_fp8_decode_chunk_and_wave_boundaries(device, bs):
     lens = [1, 511, 512, 513, 2047, 2048, 2049, 4095, 4096, 4097, 6145, 8191]
     got, want = fp8_decode_case(device, orc.BF16, 16, 8, 128, bs, lens, seed=200 + bs)
     assert_attention_close(got, want, orc.BF16, f"fp8 edges bs={bs}")
+
+
+@pytest.mark.parametrize("factor", [2.0, 3.0, 10.0])
+@pytest.mark.parametrize("code", [orc.F16, orc.BF16])
+def test_fp8_decode_large_logit_scales(device, factor, code):
+    """Logit scales of 2, 3 and 10 times 1/sqrt(head_dim) over the chunk and
+    wave edges, f16 and bf16 queries: element-wise bound (worst 0.21 of it)."""
+    lens = [1, 511, 512, 513, 2047, 2048, 2049, 4097, 6145]
+    got, want = fp8_decode_case(device, code, 16, 8, 128, 16, lens, seed=400 + int(factor) + code,
+                                softmax_scale=factor * 128 ** -0.5)
+    assert_attention_close(got, want, code, f"fp8 scale x{factor} code={code}")
 
 
 def test_fp8_decode_longest_supported_context(device):
