@@ -26,7 +26,11 @@ decode as the step runs it, right after its layer's append (step minus the
 appends alone); `append_*` is reshape_and_cache; `decode_seeds` repeats the
 decode over c3 seeds 1-5; `cpu_baseline` times the oracle's restatement of
 the reference CPU path on a bounded sample; `prefill_c4` reports the
-chunked-prefill row (append + MFMA prefill) on c4.
+chunked-prefill row (append + MFMA prefill) on c4;
+`decode_append_fused_small_batches` times the step at batches 1, 8 and 32
+with each layer's append and decode behind
+vpa_reshape_and_cache_paged_attention (one launch at those sizes) against
+the two calls. `--fused-append` runs the timed step through that entry point.
 """
 
 from __future__ import annotations
@@ -67,6 +71,11 @@ def parse():
                     help="skip the device-resident whole-step measurement")
     ap.add_argument("--seeds", default="1,2,3,4,5",
                     help="c3 seeds of the decode sweep (empty: skip it)")
+    ap.add_argument("--fused-append", action="store_true",
+                    help="run each layer's append + decode through "
+                         "vpa_reshape_and_cache_paged_attention instead of the two calls")
+    ap.add_argument("--no-small-batches", dest="small_batches", action="store_false",
+                    help="skip the small-batch comparison of the fused append + decode")
     return ap.parse_args()
 
 
@@ -156,6 +165,52 @@ def run_step(layers, ctx, w, ws):
         vpa.paged_attention(L["q"], None, None, L["kc"], L["vc"], L["bt"], ctx, None,
                             w.max_context_len, scale, 1.0, None, out=L["out"], workspace=ws,
                             planned=True)
+
+
+def run_step_fused(layers, ctx, w, ws):
+    """The same step with each layer's append and attention behind one call
+    (vpa_reshape_and_cache_paged_attention: one launch for small batches)."""
+    import vpa
+
+    scale = w.head_dim ** -0.5
+    plan_step(layers, ctx, w, ws)
+    for L in layers:
+        vpa.reshape_and_cache_paged_attention(L["q"], L["k"], L["v"], None, None, L["kc"],
+                                              L["vc"], L["bt"], ctx, w.max_context_len, scale,
+                                              out=L["out"], workspace=ws, planned=True)
+
+
+def small_batches(dev, reps, warmup, batches=(1, 8, 32)):
+    """c3's length rule at small batches (28 layers, graphs of the step): the
+    two calls per layer against vpa_reshape_and_cache_paged_attention, which
+    appends inside the decode launch at these sizes."""
+    import torch
+
+    import vpa
+    from vpa import workloads
+
+    rows = []
+    for b in batches:
+        w = workloads.c3(batch=b)
+        layers, ctx = device_tensors(w, dev)
+        ws = vpa.paged_attention_workspace(w.num_seqs, w.num_heads, w.head_dim,
+                                           w.max_context_len, dev)
+        two = graph_of(lambda: run_step(layers, ctx, w, ws))
+        one = graph_of(lambda: run_step_fused(layers, ctx, w, ws))
+        for _ in range(warmup):
+            two.replay()
+            one.replay()
+        t_two = timed_ms(two.replay, reps)
+        t_one = timed_ms(one.replay, reps)
+        rows.append({"batch": b, "mean_context": round(float(w.context_lens.mean()), 1),
+                     "two_calls_us_per_step": round(t_two * 1e3, 2),
+                     "fused_us_per_step": round(t_one * 1e3, 2),
+                     "speedup": round(t_two / t_one, 3)})
+        del layers, ws, two, one
+        torch.cuda.empty_cache()
+    return {"workload": "c3 length rule, 28 layers", "rows": rows,
+            "what": "us per decode step (graph replay): reshape_and_cache + paged_attention "
+                    "per layer, against vpa_reshape_and_cache_paged_attention per layer"}
 
 
 def timed_ms(fn, reps):
@@ -749,7 +804,8 @@ def main():
     # the step as vASR runs decode on the GPU: one HIP graph of the 28 layers
     # (vasr-paged-attn/src/cuda_graph.rs:204-225), replayed; eager launches
     # with --eager
-    step = lambda: run_step(layers, ctx, w, ws)  # noqa: E731
+    step_fn = run_step_fused if args.fused_append else run_step
+    step = lambda: step_fn(layers, ctx, w, ws)  # noqa: E731
     execution = "eager launches"
     if not args.eager:
         graph = graph_of(step)
@@ -763,7 +819,7 @@ def main():
 
     # the eager step for comparison, then each op on its own (graphs of the
     # step's layers): decode, append, decode inside the step, read ceiling
-    eager_ms = timed_ms(lambda: run_step(layers, ctx, w, ws), args.steps)
+    eager_ms = timed_ms(lambda: step_fn(layers, ctx, w, ws), args.steps)
     ops = op_timings(layers, ctx, w, ws, args.steps, args.warmup, sink=sink)
 
     dec_bytes = w.decode_bytes_per_layer()
@@ -798,6 +854,9 @@ def main():
     pf = None
     if args.prefill:
         pf = prefill_c4(dev)
+    small = None
+    if args.small_batches and w.name == "c3":
+        small = small_batches(dev, args.steps, args.warmup)
 
     line = {
         "metric": METRIC,
@@ -814,7 +873,9 @@ def main():
         "data": "synthetic (seeded)",
         "config": {
             "workload": w.name,
-            "execution": execution,
+            "execution": execution + (" (append + decode per layer behind "
+                                      "vpa_reshape_and_cache_paged_attention)"
+                                      if args.fused_append else ""),
             "num_seqs": w.num_seqs,
             "layers": nl,
             "q_heads": w.num_heads,
@@ -867,6 +928,7 @@ def main():
         "decode_fp8": f8,
         "device_step": dstep,
         "prefill_c4": pf,
+        "decode_append_fused_small_batches": small,
     }
     print(json.dumps(line), flush=True)
 

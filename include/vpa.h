@@ -229,7 +229,9 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
  * max_context_len or the table clamps, appends nothing.
  * With bf16 / f16 caches (the query's type), head_dim 128 with blocks of 16
  * or 32 tokens or head_dim 64 with 32 (a (block, head) tile of at least
- * 2 KiB) and at most 48 sequences, the append runs inside the decode launch: the wave that
+ * 2 KiB) and at most 48 sequences (the environment variable
+ * VPA_FUSED_APPEND_MAX_SEQS, read once, sets another bound), the append runs
+ * inside the decode launch: the wave that
  * reads a sequence's last block puts the new token into the K and V tiles
  * it holds and writes whole 32-byte sectors back (the value tile whole, the
  * key units of the token and its sector neighbour). Otherwise (larger

@@ -32,6 +32,7 @@
 // Every HBM access is a whole 1 KiB wave-wide run of 16-byte vectors.
 
 #include <math.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <type_traits>
@@ -1427,10 +1428,23 @@ bool decode_supported(int dtype, int head_dim, int block_size, int group) {
          (head_dim * block_size / x) % 64 == 0 && (group == 1 || group == 2 || group == 4);
 }
 
+// kFusedAppendMaxSeqs, or VPA_FUSED_APPEND_MAX_SEQS from the environment
+// (read once): the crossover depends on the lengths and the part.
+int fused_append_max_seqs() {
+  static const int v = [] {
+    const char* e = getenv("VPA_FUSED_APPEND_MAX_SEQS");
+    if (e == nullptr || *e == '\0') return kFusedAppendMaxSeqs;
+    char* end = nullptr;
+    const long n = strtol(e, &end, 10);
+    return (end != e && *end == '\0' && n >= 0 && n <= 65535) ? (int)n : kFusedAppendMaxSeqs;
+  }();
+  return v;
+}
+
 bool decode_fuses_append(int dtype, int cache_dtype, int head_dim, int block_size,
                          int num_seqs) {
   return cache_dtype == dtype && decode_uses_rows_kernel(dtype, head_dim) &&
-         fused_append_shape(head_dim, block_size) && num_seqs <= kFusedAppendMaxSeqs;
+         fused_append_shape(head_dim, block_size) && num_seqs <= fused_append_max_seqs();
 }
 
 bool decode_uses_rows_kernel(int dtype, int head_dim) {

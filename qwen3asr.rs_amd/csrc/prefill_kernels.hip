@@ -670,32 +670,30 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   static_assert(SUB * NBT <= 32, "presence bits of a step");
 
   // one pipeline step: wait for step t's tiles, refill the stage step t-1
-  // used with step t + 1, compute step t. The block ids travel a step ahead
-  // of their DMAs: the ids of step t + 1 were loaded, as one vector load
-  // (lane i < NB holds id i), right after the DMAs of step t were issued, so
-  // the wait for those DMAs covers them; here they are read back with
-  // v_readlane, step t + 1's DMAs are issued, and the ids of step t + 2 are
-  // loaded into idv behind them. No scalar load is in flight inside the
-  // loop, so the LDS operand waits (lgkmcnt) wait for LDS reads only. The
-  // masks of step t need only which of its blocks are inside the pool (pres,
-  // worked out when its DMAs were issued; pres_next gets step t + 1's).
+  // used with step t + 1, compute step t. The block ids travel ahead of the
+  // steps: pi (step t + 1, for the DMAs issued here) was loaded one step
+  // earlier and the ids of step t + 2 are loaded into pf here, so no step
+  // waits for a table load; the masks of step t need only which of its
+  // blocks are inside the pool (pres, worked out when its DMAs were issued;
+  // pres_next gets step t + 1's).
   // (With four blocks per tile the DMAs load their block ids from the table
-  // themselves: each step then loads its own ids, before its waits, for the
-  // masks, and idv is not used.)
+  // themselves and the registers of two steps' ids would not fit the larger
+  // shapes: each step then loads its own ids, before its waits, for the
+  // masks, and pi / pf are not used.)
   constexpr bool kCarryIds = NBT <= 2;
-  auto load_ids = [&](int t) -> uint32_t {
-    return bt[min(t * SUB * KT / BS + lane % NB, last_blk)];
-  };
-  auto step = [&](auto sc, int t, uint32_t pres, uint32_t& idv, uint32_t& pres_next) {
+  auto step = [&](auto sc, int t, uint32_t pres, const uint32_t (&pi)[SUB][NBT],
+                  uint32_t (&pf)[SUB][NBT], uint32_t& pres_next) {
     if (t >= n_steps) return;
     constexpr int S = decltype(sc)::value;
     const bool refill = t + 1 < n_steps;
-    if constexpr (!kCarryIds) {
+    if constexpr (kCarryIds) {
+      if (t + 2 < n_steps) step_blocks(t + 2, pf);
+    } else {
       uint32_t own[SUB][NBT];
       step_blocks(t, own);
       pres = step_present(own);
     }
-    wait_vmcnt<0>();  // step t's DMAs and step t + 1's ids (the only loads in flight)
+    wait_vmcnt<0>();  // step t's DMAs (the only ones in flight)
     // step t is in LDS for every wave, and every wave is done with step t-1.
     // A bare s_barrier: __syncthreads() would also fence this wave's LDS
     // writes, i.e. wait for all of its outstanding DMAs; the explicit vmcnt
@@ -721,28 +719,23 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
       asm volatile("" ::: "memory");
     }
     if (refill) {
-      uint32_t pi[SUB][NBT] = {};
-      if constexpr (kCarryIds) {
-#pragma unroll
-        for (int i = 0; i < NB; ++i)
-          pi[i / NBT][i % NBT] = __builtin_amdgcn_readlane(idv, i);
-        pres_next = step_present(pi);
-      }
+      if constexpr (kCarryIds) pres_next = step_present(pi);
       issue(Int<1 - S>{}, t + 1, pi);
-      if (kCarryIds && t + 2 < n_steps) idv = load_ids(t + 2);
     }
     compute(sc, t, vmask);
   };
   if (n_steps > 0) {
-    uint32_t i0[SUB][NBT] = {};
-    step_blocks(0, i0);
-    uint32_t p0 = step_present(i0), p1 = 0;
-    issue(Int<0>{}, 0, i0);
-    uint32_t idv = 0;  // ids of the step whose DMAs come next
-    if (kCarryIds && 1 < n_steps) idv = load_ids(1);
+    // ids of the step whose DMAs come next (x at even steps, y at odd ones)
+    // and of the one after it; presence bits of the current and next step
+    uint32_t ix[SUB][NBT] = {}, iy[SUB][NBT] = {};
+    uint32_t p0 = 0, p1 = 0;
+    step_blocks(0, ix);
+    p0 = step_present(ix);
+    issue(Int<0>{}, 0, ix);
+    if (kCarryIds && 1 < n_steps) step_blocks(1, ix);
     for (int t0 = 0; t0 < n_steps; t0 += 2) {
-      step(Int<0>{}, t0, p0, idv, p1);
-      step(Int<1>{}, t0 + 1, p1, idv, p0);
+      step(Int<0>{}, t0, p0, ix, iy, p1);      // loads the ids of t0 + 2 into iy
+      step(Int<1>{}, t0 + 1, p1, iy, ix, p0);  // loads the ids of t0 + 3 into ix
     }
   }
 

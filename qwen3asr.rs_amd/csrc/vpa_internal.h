@@ -56,7 +56,8 @@ struct DecodeAppend {
   int64_t value_token_stride;
 };
 
-// Largest batch whose decode append runs inside the decode launch.
+// Largest batch whose decode append runs inside the decode launch (the
+// environment variable VPA_FUSED_APPEND_MAX_SEQS, read once, overrides it).
 constexpr int kFusedAppendMaxSeqs = 48;
 // True when vpa_reshape_and_cache_paged_attention runs its append inside the
 // decode launch (16-bit cache of the query's type, head_dim 64 / 128 with a
