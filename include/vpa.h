@@ -355,8 +355,9 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
  * v_scale, scale, softcapping = 1) of vasr-paged-attn/src/metal/
  * varlen_prefill.rs:284-420.
  *
- * query/out: [total_query_rows, num_heads, head_dim] packed, bf16 or f16 (the
- * reference's flash path takes no f32, attention.rs:562). Sequence s owns
+ * query/out: [total_query_rows, num_heads, head_dim] packed, bf16, f16 or
+ * f32 (the reference's flash path takes no f32, attention.rs:562; its Metal
+ * prefill does, prefill_paged_attn.metal:1606, 1610). Sequence s owns
  * query rows cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1 (n_s rows) and its first
  * L_s = context_lens[s] cached tokens (PagedInputMetadata::context_lens of a
  * prefill, paged_kv_cache.rs:525-532), the new rows' K/V included (append
@@ -370,15 +371,16 @@ int vpa_gather_kv_cache(void* out_key, void* out_value, const void* key_cache,
  * max_t s_t): denom_eps 0 is the flash attention of the CUDA path, 1e-6 the
  * Metal kernel (prefill_paged_attn.metal:1300); it must be finite and >= 0.
  * Head dims 64, 96, 128, 192 and 256 (the Metal kernel's set,
- * varlen_prefill.rs:15), 1, 2 or 4 query heads per kv head.
- * cache_dtype equals dtype (block_size 8, 16 or 32), or is
- * VPA_DTYPE_FP8_E4M3 (block_size 8, 16 or 32) for bf16/f16 queries; head_dim
- * 96 needs 16- or 32-token blocks at 16 bits and 32-token blocks at fp8, fp8
- * at 8-token blocks head_dim 128 or 256. The
- * cache is read as byte *
- * k_scale / byte * v_scale (the Metal kernel's fp8 path,
- * prefill_paged_attn.metal:698-769), converted to the query type in
- * registers. Needs no workspace; safe under stream capture.
+ * varlen_prefill.rs:15), block_size 8, 16 or 32, any number of query heads
+ * per kv head; cache_dtype equals dtype or is VPA_DTYPE_FP8_E4M3 (for any
+ * query type). bf16 / f16 queries with 1, 2 or 4 query heads per kv head
+ * run on the MFMA kernel where a (block, head) tile is a whole number of
+ * 1 KiB DMAs (head_dim 96 at 16- or 32-token blocks for 16 bits, 32-token
+ * blocks for fp8; fp8 at 8-token blocks head_dim 128 or 256); every other
+ * configuration, f32 included, on a vector-ALU kernel with f32 arithmetic.
+ * An fp8 cache is read as byte * k_scale / byte * v_scale (the Metal
+ * kernel's fp8 path, prefill_paged_attn.metal:698-769, 797-800), converted
+ * to the query type. Needs no workspace; safe under stream capture.
  */
 int vpa_chunked_prefill_paged_attention(
     void* out, const void* query, const float* k_scale, const float* v_scale,

@@ -620,7 +620,9 @@ int vpa_chunked_prefill_paged_attention(
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: denom_eps must be finite and >= 0, got %g", op,
                 (double)denom_eps);
   const bool fp8 = cache_dtype == VPA_DTYPE_FP8_E4M3;
-  if (dtype != cache_dtype && !(fp8 && (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16)))
+  if (!is_float_dtype(dtype))
+    return fail(VPA_ERR_UNSUPPORTED, "%s: unsupported query dtype %s", op, dtype_name(dtype));
+  if (dtype != cache_dtype && !fp8)
     return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from query dtype %s", op,
                 dtype_name(cache_dtype), dtype_name(dtype));
   int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
@@ -639,18 +641,19 @@ int vpa_chunked_prefill_paged_attention(
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: num_heads=%d not a multiple of num_kv_heads=%d",
                 op, num_heads, num_kv_heads);
   const int group = num_heads / num_kv_heads;
-  if (!prefill_supported(dtype, cache_dtype, head_dim, block_size, group))
+  // the MFMA kernel where it is built for the shape, else the vector kernel
+  const bool mfma = prefill_supported(dtype, cache_dtype, head_dim, block_size, group);
+  if (!mfma && !prefill_vector_supported(dtype, cache_dtype, head_dim, block_size))
     return fail(VPA_ERR_UNSUPPORTED,
-                "%s: no MFMA kernel for dtype=%s cache=%s head_dim=%d block_size=%d group=%d "
-                "(bf16/f16, head_dim 64/96/128/192/256, block_size 8/16/32, 1/2/4 query "
-                "heads per kv head; head_dim 96 needs 16- or 32-token blocks at 16 bits and "
-                "32-token blocks at fp8; fp8 at 8-token blocks: head_dim 128/256)",
-                op, dtype_name(dtype), dtype_name(cache_dtype), head_dim, block_size, group);
+                "%s: no kernel for dtype=%s cache=%s head_dim=%d block_size=%d (head_dim "
+                "64/96/128/192/256, block_size 8/16/32)",
+                op, dtype_name(dtype), dtype_name(cache_dtype), head_dim, block_size);
   if (num_seqs == 0 || max_query_len == 0 || total_query_rows == 0) return VPA_OK;
   {
     const int ppb = prefill_positions_per_workgroup(group);
     const int64_t grid =
-        (int64_t)num_seqs * ((max_query_len + ppb - 1) / ppb) * (int64_t)num_kv_heads;
+        mfma ? (int64_t)num_seqs * ((max_query_len + ppb - 1) / ppb) * (int64_t)num_kv_heads
+             : prefill_vector_workgroups(num_seqs, max_query_len, group, num_kv_heads);
     if (grid > ((int64_t)1 << 31) - 1)
       return fail(VPA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups exceeds 2^31-1", op,
                   (long long)grid);
@@ -668,14 +671,13 @@ int vpa_chunked_prefill_paged_attention(
                 block_table_stride, max_kv_len, block_size);
   CacheGeom g{num_kv_heads, head_dim, block_size, num_blocks, cache_block_stride,
               cache_head_stride};
-  return hip_status(op, launch_prefill_paged(dtype, cache_dtype, out, query, key_cache,
-                                             value_cache, block_tables, block_table_stride,
-                                             cu_seqlens_q, context_lens, num_seqs, max_query_len,
-                                             max_kv_len, total_query_rows, softmax_scale,
-                                             denom_eps, causal,
-                                             num_heads, g, fp8 ? k_scale : nullptr,
-                                             fp8 ? v_scale : nullptr,
-                                             static_cast<hipStream_t>(stream)));
+  const auto launch = mfma ? launch_prefill_paged : launch_prefill_vector;
+  return hip_status(op, launch(dtype, cache_dtype, out, query, key_cache, value_cache,
+                               block_tables, block_table_stride, cu_seqlens_q, context_lens,
+                               num_seqs, max_query_len, max_kv_len, total_query_rows,
+                               softmax_scale, denom_eps, causal, num_heads, g,
+                               fp8 ? k_scale : nullptr, fp8 ? v_scale : nullptr,
+                               static_cast<hipStream_t>(stream)));
 }
 
 int vpa_argmax_rows(const void* logits, int64_t row_stride, int32_t vocab, int32_t num_rows,

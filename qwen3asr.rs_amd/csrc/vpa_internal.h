@@ -173,6 +173,22 @@ hipError_t launch_prefill_paged(int dtype, int cache_dtype, void* out, const voi
                                 const float* k_scale, const float* v_scale,
                                 hipStream_t stream);
 
+// The vector-ALU prefill (prefill_vector_kernels.hip): f32 queries over f32
+// or fp8 caches, any number of query heads per kv head, and the 16-bit
+// shapes the MFMA kernel does not take. Same arguments as launch_prefill_paged.
+bool prefill_vector_supported(int dtype, int cache_dtype, int head_dim, int block_size);
+int64_t prefill_vector_workgroups(int32_t num_seqs, int32_t max_query_len, int32_t group,
+                                  int32_t num_kv_heads);
+hipError_t launch_prefill_vector(int dtype, int cache_dtype, void* out, const void* query,
+                                 const void* key_cache, const void* value_cache,
+                                 const uint32_t* block_tables, int32_t block_table_stride,
+                                 const uint32_t* cu_seqlens_q, const uint32_t* context_lens,
+                                 int32_t num_seqs, int32_t max_query_len, int32_t max_kv_len,
+                                 int64_t total_query_rows, float scale, float denom_eps,
+                                 int32_t causal, int32_t num_heads, const CacheGeom& g,
+                                 const float* k_scale, const float* v_scale,
+                                 hipStream_t stream);
+
 // Query positions one prefill workgroup covers for a GQA group size.
 int prefill_positions_per_workgroup(int group);
 // True when the MFMA prefill kernel is compiled for this combination.

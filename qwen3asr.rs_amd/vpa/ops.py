@@ -342,7 +342,7 @@ def paged_attention_varlen_prefill(q: torch.Tensor, key_cache: torch.Tensor,
     (``vasr-paged-attn/src/metal/varlen_prefill.rs:284-295``), which is
     non-causal; ``causal=True`` gives the bottom-right causal attention that
     the CUDA build computes with gather_kv_cache + flash varlen
-    (``thinker_text.rs:1344-1365``). ``q`` is [total_q, H, D] bf16/f16;
+    (``thinker_text.rs:1344-1365``). ``q`` is [total_q, H, D] bf16/f16/f32;
     sequence s owns rows cu_seqlens_q[s]..cu_seqlens_q[s+1]-1 and the first
     context_lens[s] cached tokens (its own new tokens included). The maxima
     size the grid; a caller that knows them on the host passes them to skip

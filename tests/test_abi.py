@@ -190,16 +190,10 @@ def pf_call(**over):
 
 
 @pytest.mark.parametrize("over,code,needle", [
-    (dict(dtype=_lib.DTYPE_F32, cdtype=_lib.DTYPE_F32, bstride=8 * 128 * 16 * 2,
-          hstride=128 * 16 * 2), _lib.VPA_ERR_UNSUPPORTED, "no MFMA kernel"),
-    (dict(d=96, bs=8, bstride=8 * 96 * 8, hstride=96 * 8), _lib.VPA_ERR_UNSUPPORTED,
-     "no MFMA kernel"),
     (dict(d=80, bstride=8 * 80 * 16, hstride=80 * 16), _lib.VPA_ERR_UNSUPPORTED,
      "no kernel for dtype"),
-    (dict(cdtype=_lib.DTYPE_FP8_E4M3, ks=FAKE, vs=FAKE, d=96, bs=16, bstride=8 * 96 * 16,
-          hstride=96 * 16), _lib.VPA_ERR_UNSUPPORTED, "no MFMA kernel"),
-    (dict(h=64), _lib.VPA_ERR_UNSUPPORTED, "no MFMA kernel"),
     (dict(h=12), _lib.VPA_ERR_INVALID_ARGUMENT, "multiple"),
+    (dict(dtype=5, cdtype=5), _lib.VPA_ERR_UNSUPPORTED, "query dtype"),
     (dict(cdtype=_lib.DTYPE_F16), _lib.VPA_ERR_UNSUPPORTED, "differs"),
     (dict(bts=10), _lib.VPA_ERR_INVALID_ARGUMENT, "block_table_stride"),
     (dict(cuq=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
@@ -213,6 +207,26 @@ def test_prefill_host_validation(over, code, needle):
     rc, msg = pf_call(**over)
     assert rc == code, msg
     assert needle in msg
+
+
+@pytest.mark.parametrize("over", [
+    dict(dtype=_lib.DTYPE_F32, cdtype=_lib.DTYPE_F32, bstride=8 * 128 * 16 * 2,
+         hstride=128 * 16 * 2),
+    dict(dtype=_lib.DTYPE_F32, cdtype=_lib.DTYPE_FP8_E4M3, ks=FAKE, vs=FAKE,
+         bstride=8 * 128 * 16, hstride=128 * 16),
+    dict(d=96, bs=8, bstride=8 * 96 * 8, hstride=96 * 8),
+    dict(cdtype=_lib.DTYPE_FP8_E4M3, ks=FAKE, vs=FAKE, d=96, bs=16, bstride=8 * 96 * 16,
+         hstride=96 * 16),
+    dict(h=64), dict(h=24), dict(h=128)])
+def test_prefill_vector_kernel_configs_pass_validation(over):
+    """The configurations the MFMA prefill is not built for go to the vector
+    kernel: f32 queries over f32 and fp8 caches (the Metal prefill's `float`
+    and `float, uint8_t` instances), the 16-bit / fp8 head-dim and block-size
+    pairs without whole 1 KiB DMAs, and 8, 3 and 16 query heads per kv head.
+    They pass every host check; an empty batch then returns before any
+    launch."""
+    rc, msg = pf_call(maxq=0, **over)
+    assert rc == 0, msg
 
 
 @pytest.mark.parametrize("d,bs,fp8", [(96, 16, False), (96, 32, False), (192, 8, False),
@@ -358,11 +372,11 @@ def test_gather_and_prefill_fp8_validation():
     # prefill over an fp8 cache: validation only (no device here)
     rc, msg = pf_call(cdtype=FP8, **F8_STRIDES)
     assert rc == _lib.VPA_ERR_INVALID_ARGUMENT and "k_scale" in msg, msg
-    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, dtype=_lib.DTYPE_F32, **F8_STRIDES)
-    assert rc == _lib.VPA_ERR_UNSUPPORTED and "differs" in msg, msg
+    rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, dtype=_lib.DTYPE_F32, maxq=0, **F8_STRIDES)
+    assert rc == 0, msg
     rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bs=8, bstride=8 * 64 * 8,
-                      hstride=64 * 8)
-    assert rc == _lib.VPA_ERR_UNSUPPORTED and "no MFMA kernel" in msg, msg
+                      hstride=64 * 8, maxq=0)
+    assert rc == 0, msg
     # fp8 at 8-token blocks: head_dim 128 (decode and prefill) and 256 (prefill)
     rc, msg = pf_call(cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bstride=8 * 128 * 8, hstride=128 * 8,
                       maxq=0)
