@@ -148,6 +148,9 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * at graph capture is fine as long as it is >= every context_len).
  * alibi_slopes and sinks must be NULL and softcapping must be 1.0 (the only
  * values vASR passes); anything else returns VPA_ERR_UNSUPPORTED.
+ * Any number of query heads per kv head: the kernels serve 1, 2 or 4 per
+ * kv head, and a larger G runs as G / 4 (or / 2, / 1 where 4 does not
+ * divide G) replicas of each kv head, each reading that head's tiles.
  * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 with a bf16 or f16
  * query (head_dim 64 or 128 with block_size 16 or 32, head_dim 128 with
  * block_size 8): K and V are then read as

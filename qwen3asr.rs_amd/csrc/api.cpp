@@ -288,9 +288,6 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: num_heads=%d not a multiple of num_kv_heads=%d",
                 op, num_heads, num_kv_heads);
   const int group = num_heads / num_kv_heads;
-  if (!(group == 1 || group == 2 || group == 4))
-    return fail(VPA_ERR_UNSUPPORTED,
-                "%s: no kernel for %d query heads per kv head (supported: 1, 2, 4)", op, group);
   if (!decode_supported(dtype, head_dim, block_size, group))
     return fail(VPA_ERR_UNSUPPORTED,
                 "%s: no decode kernel for %s head_dim=%d block_size=%d (a (block, head) tile "
@@ -309,9 +306,10 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
     const int64_t parts =
         std::max<int64_t>(1, ((int64_t)max_context_len + kDecodeMinPartitionTokens - 1) /
                                  kDecodeMinPartitionTokens);
-    if ((int64_t)num_seqs * parts * num_kv_heads > ((int64_t)1 << 25))
+    const int64_t units = (int64_t)num_heads / decode_kernel_group(group);
+    if ((int64_t)num_seqs * parts * units > ((int64_t)1 << 25))
       return fail(VPA_ERR_UNSUPPORTED,
-                  "%s: num_seqs * ceil(max_context_len/%d) * num_kv_heads exceeds 2^25", op,
+                  "%s: num_seqs * ceil(max_context_len/%d) * kv head replicas exceeds 2^25", op,
                   kDecodeMinPartitionTokens);
   }
   if (out == nullptr || query == nullptr || block_tables == nullptr || context_lens == nullptr)
@@ -378,7 +376,7 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
   // and the other configurations run the append kernel on the derived slots,
   // then the decode: the same bytes and results either way.
   const bool fuse = append != nullptr &&
-                    decode_fuses_append(dtype, cache_dtype, head_dim, block_size, num_seqs);
+                    decode_fuses_append(dtype, cache_dtype, head_dim, block_size, num_seqs, group);
   if (append != nullptr && !fuse) {
     LastSlots last;
     last.block_tables = block_tables;

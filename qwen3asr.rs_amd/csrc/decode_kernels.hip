@@ -87,7 +87,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
     int32_t block_table_stride, const uint32_t* __restrict__ context_lens, int32_t max_ctx,
     float scale, int32_t num_heads, int64_t num_blocks, int64_t block_stride,
     int64_t head_stride, float* __restrict__ part_out, float* __restrict__ part_max,
-    float* __restrict__ part_sum, int32_t max_parts) {
+    float* __restrict__ part_sum, int32_t max_parts, int32_t kv_rep) {
   constexpr int X = pack_x<T>();
   constexpr int LPT = 64 / BS;          // lanes per token in the key tile
   constexpr int KPL = D * BS / X / 64;  // key (and value) vectors per lane per block
@@ -158,7 +158,9 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
     else return qv[g][k];
   };
 
-  const int64_t head_off = (int64_t)j * head_stride;
+  // j counts kv_rep replicas of every kv head (kv_rep > 1: more query heads
+  // per kv head than G), so its cache head is j / kv_rep
+  const int64_t head_off = (int64_t)(j / kv_rep) * head_stride;
   const uint4* kbase = reinterpret_cast<const uint4*>(key_cache + head_off);
   const uint4* vbase = reinterpret_cast<const uint4*>(value_cache + head_off);
   const int64_t bstride_v = block_stride / X;  // block stride in 16-byte vectors
@@ -518,7 +520,8 @@ void paged_decode_rows_kernel(
     int32_t max_parts, const uint2* __restrict__ items, const uint32_t* __restrict__ queue,
     int32_t num_seqs, int32_t max_ctx, int32_t cap_tokens, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const T* __restrict__ new_key,
-    const T* __restrict__ new_value, int64_t new_key_stride, int64_t new_value_stride) {
+    const T* __restrict__ new_value, int64_t new_key_stride, int64_t new_value_stride,
+    int32_t kv_rep) {
   constexpr bool kF8 = std::is_same_v<C, fp8_t>;
   static_assert(kF8 || std::is_same_v<C, T>, "cache type is the query type or fp8");
   static_assert(!(kAppend && kF8), "the fused append writes 16-bit caches");
@@ -653,7 +656,9 @@ void paged_decode_rows_kernel(
                     : new_value + (int64_t)s * new_value_stride + (int64_t)j * D +
                           (lane - NR) * 8);
 
-    const int64_t head_off = (int64_t)j * head_stride;
+    // j counts kv_rep replicas of every kv head (more query heads per kv
+    // head than G): its cache head is j / kv_rep
+    const int64_t head_off = (int64_t)(j / kv_rep) * head_stride;
     const uint4* kbase = reinterpret_cast<const uint4*>(key_cache + head_off);
     const uint4* vbase = reinterpret_cast<const uint4*>(value_cache + head_off);
     const int64_t bstride_v = block_stride / X;
@@ -1143,7 +1148,7 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
                          ws.max_parts, ws.items, ws.queue, num_seqs, max_ctx, cap_tokens,
                          k_scale, v_scale, static_cast<const T*>(app->key),
                          static_cast<const T*>(app->value), app->key_token_stride,
-                         app->value_token_stride);
+                         app->value_token_stride, g.kv_rep);
     }
   }
   if (kFp8 || !fused_append_shape(D, BS) || app == nullptr) {
@@ -1154,7 +1159,7 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
                        g.num_blocks, g.block_stride, g.head_stride, ws.part_out, ws.max_parts,
                        ws.items, ws.queue, num_seqs, max_ctx, cap_tokens, k_scale, v_scale,
                        static_cast<const T*>(nullptr), static_cast<const T*>(nullptr),
-                       (int64_t)0, (int64_t)0);
+                       (int64_t)0, (int64_t)0, g.kv_rep);
   }
   e = hipGetLastError();
   if (e != hipSuccess || max_chunks <= 1) return e;
@@ -1203,7 +1208,7 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
                      static_cast<T*>(out), static_cast<const T*>(q), static_cast<const T*>(kc),
                      static_cast<const T*>(vc), bt, bts, cl, max_ctx, scale, num_heads,
                      g.num_blocks, g.block_stride, g.head_stride, ws.part_out, ws.part_max,
-                     ws.part_sum, ws.max_parts);
+                     ws.part_sum, ws.max_parts, g.kv_rep);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_parts <= 1) return e;
   dim3 rgrid((unsigned)num_heads, (unsigned)num_seqs);
@@ -1425,8 +1430,10 @@ hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t m
 bool decode_supported(int dtype, int head_dim, int block_size, int group) {
   const int x = dtype == VPA_DTYPE_F32 ? 4 : 8;
   return dtype != VPA_DTYPE_FP8_E4M3 && cache_kernels_supported(dtype, head_dim, block_size) &&
-         (head_dim * block_size / x) % 64 == 0 && (group == 1 || group == 2 || group == 4);
+         (head_dim * block_size / x) % 64 == 0 && group >= 1;
 }
+
+int decode_kernel_group(int group) { return group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1; }
 
 // kFusedAppendMaxSeqs, or VPA_FUSED_APPEND_MAX_SEQS from the environment
 // (read once): the crossover depends on the lengths and the part.
@@ -1442,9 +1449,10 @@ int fused_append_max_seqs() {
 }
 
 bool decode_fuses_append(int dtype, int cache_dtype, int head_dim, int block_size,
-                         int num_seqs) {
+                         int num_seqs, int group) {
   return cache_dtype == dtype && decode_uses_rows_kernel(dtype, head_dim) &&
-         fused_append_shape(head_dim, block_size) && num_seqs <= fused_append_max_seqs();
+         fused_append_shape(head_dim, block_size) && num_seqs <= fused_append_max_seqs() &&
+         decode_kernel_group(group) == group;
 }
 
 bool decode_uses_rows_kernel(int dtype, int head_dim) {
@@ -1518,15 +1526,21 @@ hipError_t launch_paged_decode(int dtype, int cache_dtype, void* out, const void
                                int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
                                const DecodeWorkspace& ws, hipStream_t stream,
                                const DecodeAppend* append) {
-  const int group = num_heads / g.num_kv_heads;
+  // G query heads per kv head run as kv_rep = G / group replicas of each kv
+  // head, group (1, 2 or 4) query heads each: every replica reads its kv
+  // head's tiles (kv_rep times the K/V bytes of one pass, for G of 8 or more)
+  const int group = decode_kernel_group(num_heads / g.num_kv_heads);
+  CacheGeom gv = g;
+  gv.kv_rep = num_heads / g.num_kv_heads / group;
+  gv.num_kv_heads = g.num_kv_heads * gv.kv_rep;
   if (cache_dtype == VPA_DTYPE_FP8_E4M3)
     return dispatch_decode_fp8(dtype, g.head_dim, g.block_size, group, out, query, key_cache,
                                value_cache, block_tables, block_table_stride, context_lens,
-                               max_context_len, scale, num_seqs, num_heads, g, ws, stream,
+                               max_context_len, scale, num_seqs, num_heads, gv, ws, stream,
                                k_scale, v_scale, append);
   return dispatch_decode(dtype, g.head_dim, g.block_size, group, out, query, key_cache,
                          value_cache, block_tables, block_table_stride, context_lens,
-                         max_context_len, scale, num_seqs, num_heads, g, ws, stream, k_scale,
+                         max_context_len, scale, num_seqs, num_heads, gv, ws, stream, k_scale,
                          v_scale, append);
 }
 

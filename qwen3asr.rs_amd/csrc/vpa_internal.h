@@ -22,6 +22,10 @@ struct CacheGeom {
   int64_t num_blocks;
   int64_t block_stride;  // elements
   int64_t head_stride;   // elements
+  // decode only: num_kv_heads counts kv_rep replicas of every cache head
+  // (head j reads cache head j / kv_rep), for more query heads per kv head
+  // than a kernel instance serves
+  int32_t kv_rep = 1;
 };
 
 // Decode split-K partition length in tokens of the generic decode kernel (a
@@ -63,7 +67,10 @@ constexpr int kFusedAppendMaxSeqs = 48;
 // decode launch (16-bit cache of the query's type, head_dim 64 / 128 with a
 // (block, head) tile of at least 2 KiB, at most kFusedAppendMaxSeqs sequences).
 bool decode_fuses_append(int dtype, int cache_dtype, int head_dim, int block_size,
-                         int num_seqs);
+                         int num_seqs, int group);
+// Query heads per kv head a decode kernel instance serves for G query heads
+// per kv head (4, 2 or 1, dividing G); larger G runs G / that replicas.
+int decode_kernel_group(int group);
 
 // Compute units of the current device (cached per device).
 int device_cu_count();

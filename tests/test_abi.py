@@ -125,7 +125,8 @@ def pa_call(**over):
     (dict(sinks=FAKE), _lib.VPA_ERR_UNSUPPORTED, "sinks"),
     (dict(softcap=30.0), _lib.VPA_ERR_UNSUPPORTED, "softcapping"),
     (dict(h=12), _lib.VPA_ERR_INVALID_ARGUMENT, "multiple"),
-    (dict(h=64), _lib.VPA_ERR_UNSUPPORTED, "query heads per kv head"),
+    (dict(h=64), _lib.VPA_ERR_WORKSPACE, "workspace"),  # 8 per kv head: passes the shape checks
+    (dict(h=24), _lib.VPA_ERR_WORKSPACE, "workspace"),
     (dict(bts=10), _lib.VPA_ERR_INVALID_ARGUMENT, "block_table_stride"),
     (dict(q=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
     (dict(cdtype=_lib.DTYPE_F16), _lib.VPA_ERR_UNSUPPORTED, "differs"),
@@ -280,7 +281,7 @@ def plan_call(**over):
     (dict(ws_bytes=16), _lib.VPA_ERR_WORKSPACE, "workspace"),
     (dict(ws=FAKE * 256 + 16), _lib.VPA_ERR_INVALID_ARGUMENT, "256-byte"),
     (dict(h=12), _lib.VPA_ERR_INVALID_ARGUMENT, "bad sizes"),
-    (dict(h=64), _lib.VPA_ERR_UNSUPPORTED, "no decode kernel"),
+    (dict(d=80), _lib.VPA_ERR_UNSUPPORTED, "no decode kernel"),
     (dict(cl=None), _lib.VPA_ERR_INVALID_ARGUMENT, "non-null"),
     (dict(bts=10), _lib.VPA_ERR_INVALID_ARGUMENT, "block_table_stride"),
     (dict(b=70000), _lib.VPA_ERR_UNSUPPORTED, "num_seqs"),

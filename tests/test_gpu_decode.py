@@ -204,6 +204,17 @@ def test_decode_large_logit_scales(device, factor, code, d, h, kvh, bs):
         assert_attention_close(got, want, code, what)
 
 
+@pytest.mark.parametrize("h,kvh", [(64, 8), (24, 8), (32, 2), (16, 1), (12, 4)])
+@pytest.mark.parametrize("code,d,bs", [(orc.BF16, 128, 16), (orc.F16, 64, 32), (orc.F32, 128, 16),
+                                       (orc.BF16, 96, 16), (orc.BF16, 128, 8)])
+def test_decode_query_heads_per_kv_head(device, h, kvh, code, d, bs):
+    """8, 3, 16 and 16 query heads per kv head (the kernels serve 1, 2 or 4;
+    larger groups run as replicas of each kv head) over the chunk edges."""
+    lens = [1, 17, 511, 512, 2049, 4097]
+    got, want = decode_case(device, code, h, kvh, d, bs, lens, seed=h + kvh + d + bs + code)
+    assert_attention_close(got, want, code, f"h={h} kvh={kvh} code={code} d={d} bs={bs}")
+
+
 def test_decode_long_context_split_k(device):
     """Contexts spanning many split-K partitions (up to 8192 tokens)."""
     lens = [8192, 4097, 4096, 2049, 333]

@@ -177,6 +177,15 @@ def test_fp8_decode_large_logit_scales(device, factor, code):
     assert_attention_close(got, want, code, f"fp8 scale x{factor} code={code}")
 
 
+@pytest.mark.parametrize("h,kvh", [(64, 8), (24, 8)])
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+def test_fp8_decode_query_heads_per_kv_head(device, h, kvh, code):
+    """8 and 3 query heads per kv head over an fp8 cache with scales."""
+    got, want = fp8_decode_case(device, code, h, kvh, 128, 16, [1, 300, 2049, 4097],
+                                seed=h + kvh + code, scales=(0.6, 1.7))
+    assert_attention_close(got, want, code, f"fp8 h={h} kvh={kvh} code={code}")
+
+
 def test_fp8_decode_longest_supported_context(device):
     """A 262 144-token context over an fp8 cache (the longest the decode
     takes: 128 chunks merged) beside a one-token sequence, with scales."""
