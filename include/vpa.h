@@ -76,11 +76,11 @@ const char* vpa_version(void);
  * non-zero. Fills key_shape[5] and value_shape[4].
  *
  * The ops below take head_dim 64, 96, 128, 192 or 256 and block_size 8, 16
- * or 32 (the append and the gather every combination; decode and prefill
- * need a (block, head) tile of a whole number of KiB, head_dim * block_size
- * / x a multiple of 64, so head_dim 96 needs 16- or 32-token blocks at 16
- * bits and 32-token blocks at fp8, and fp8 at 8-token blocks head_dim 128
- * or 256). Other shapes return VPA_ERR_UNSUPPORTED.
+ * or 32: the append, the gather and the chunked prefill every combination;
+ * decode a (block, head) tile of a whole number of KiB, head_dim *
+ * block_size / x a multiple of 64 (head_dim 96 needs 16- or 32-token
+ * blocks at 16 bits), and over fp8 caches the shapes listed at
+ * vpa_paged_attention. Other shapes return VPA_ERR_UNSUPPORTED.
  */
 int vpa_cache_layout(int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                      int64_t num_blocks, int32_t cache_dtype, int64_t* key_shape,
@@ -152,8 +152,8 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * kv head, and a larger G runs as G / 4 (or / 2, / 1 where 4 does not
  * divide G) replicas of each kv head, each reading that head's tiles.
  * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 with a bf16 or f16
- * query (head_dim 64 or 128 with block_size 16 or 32, head_dim 128 with
- * block_size 8): K and V are then read as
+ * query (head_dim 64 or 128 with block_size 16 or 32, 128 or 256 with 8,
+ * 96 with 32, 192 or 256 with 16): K and V are then read as
  * (float)byte * (*k_scale) and (float)byte * (*v_scale), k_scale / v_scale
  * being device pointers to one f32 each (ignored for 16/32-bit caches).
  * workspace must hold vpa_paged_attention_workspace_size(...) bytes (always
@@ -230,16 +230,16 @@ int vpa_paged_attention_planned(void* out, const void* query, const float* k_sca
  * over its own token, where the two calls would give all of them the
  * stored one). A sequence with context_lens[s] = 0, or a context that
  * max_context_len or the table clamps, appends nothing.
- * With bf16 / f16 caches (the query's type), head_dim 128 with blocks of 16
- * or 32 tokens or head_dim 64 with 32 (a (block, head) tile of at least
- * 2 KiB) and at most 48 sequences (the environment variable
+ * With bf16 / f16 caches (the query's type), a (block, head) tile of 2 to 8
+ * KiB (head_dim 64 with blocks of 32 tokens, 128 with 16 or 32, 96 with 32,
+ * 192 with 16, 256 with 8 or 16) and at most 48 sequences (the environment variable
  * VPA_FUSED_APPEND_MAX_SEQS, read once, sets another bound), the append runs
  * inside the decode launch: the wave that
  * reads a sequence's last block puts the new token into the K and V tiles
  * it holds and writes whole 32-byte sectors back (the value tile whole, the
  * key units of the token and its sector neighbour). Otherwise (larger
  * batches, where those writes cost the bandwidth-bound decode more than the
- * append's own launch; f32 and fp8 caches; other head dims) it launches the
+ * append's own launch; f32 and fp8 caches; other shapes) it launches the
  * append kernel on the derived slots, then the decode. Arguments and errors
  * as vpa_reshape_and_cache and vpa_paged_attention (dtype: the query and
  * row type; scales as there); softcapping off, no alibi, no sinks.
@@ -277,7 +277,7 @@ int vpa_reshape_and_cache_paged_attention_planned(
  * VPA_NOALLOC_SCRATCH_MIB; `make NOALLOC_SCRATCH_MIB=<n>`), held until the
  * process ends by every process that loads the library, whether or not it
  * calls this entry point, and laid out for the kernel this configuration runs (16-bit / fp8 caches
- * with head_dim <= 128: num_seqs * num_heads * ceil(max_context_len / 2048)
+ * on the rows kernel: num_seqs * num_heads * ceil(max_context_len / 2048)
  * partial rows of (head_dim + 32) floats, 5.3 MB at batch 256 / context
  * 4096, 42 MB at batch 1024 / context 8192). A call whose layout does not
  * fit returns VPA_ERR_WORKSPACE (after the other argument checks, before

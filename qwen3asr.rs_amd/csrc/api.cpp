@@ -273,11 +273,10 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
   if (rc != VPA_OK) return rc;
   rc = check_scales(op, cache_dtype, k_scale, v_scale);
   if (rc != VPA_OK) return rc;
-  if (fp8 && !((head_dim == 64 || head_dim == 128) && (block_size == 16 || block_size == 32)) &&
-      !(fp8 && head_dim == 128 && block_size == 8))
+  if (fp8 && !decode_fp8_shape(head_dim, block_size))
     return fail(VPA_ERR_UNSUPPORTED,
-                "%s: fp8 cache needs head_dim 64 or 128 with block_size 16 or 32, or head_dim 128 "
-                "with block_size 8 (got %d, %d)",
+                "%s: fp8 cache needs head_dim 64 or 128 with block_size 16 or 32, 128 or 256 "
+                "with 8, 96 with 32, 192 or 256 with 16 (got %d, %d)",
                 op, head_dim, block_size);
   if (num_seqs < 0 || num_heads <= 0 || max_context_len < 0 || block_table_stride < 0)
     return fail(VPA_ERR_INVALID_ARGUMENT,
@@ -336,7 +335,8 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
       return fail(VPA_ERR_INVALID_ARGUMENT, "%s: key/value rows must be 16-byte aligned", op);
   }
   const int part_tokens =
-      scratch != nullptr ? decode_part_tokens(dtype, head_dim) : kDecodeMinPartitionTokens;
+      scratch != nullptr ? decode_part_tokens(dtype, head_dim, block_size)
+                         : kDecodeMinPartitionTokens;
   const size_t need =
       decode_workspace_bytes(num_seqs, num_heads, head_dim, max_context_len, part_tokens);
   if (scratch != nullptr) {

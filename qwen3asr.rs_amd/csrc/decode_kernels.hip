@@ -548,9 +548,10 @@ void paged_decode_rows_kernel(
   // value tiles the same way (lane l: row l / (BS/8) + k * 64 / (BS/8),
   // tokens (l % (BS/8)) * 8 .. +7).
   constexpr int KPL = D * BS / (X * 64);  // loads per lane per tile (K or V)
-  // 16-byte loads per lane per stage (at least one tile)
+  // 16-byte loads per lane per stage: the whole tiles that fit NV0 loads,
+  // at least one tile (head dims 96 and 192 give 3 or 6 loads per tile)
   constexpr int NV0 = kF8 ? VPA_DECODE_FP8_NV : VPA_DECODE_NV;
-  constexpr int NV = NV0 > KPL ? NV0 : KPL;
+  constexpr int NV = KPL >= NV0 ? KPL : (NV0 / KPL) * KPL;
   constexpr int LPT = 64 / BS;            // lanes per token in a key tile
   constexpr int BKS = NV / KPL;           // tiles per stage
   static_assert(KPL == NVV && KPL >= 1 && KPL <= NV && NV % KPL == 0, "stage shape");
@@ -1060,7 +1061,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
     T* __restrict__ out, const uint32_t* __restrict__ context_lens, int32_t num_seqs,
     int32_t max_ctx, int32_t cap_tokens, int32_t part_tokens, int32_t num_heads,
     const float* __restrict__ part, int32_t max_parts) {
-  constexpr int DPL = D / 64;
+  constexpr int DPL = (D + 63) / 64;  // output elements per lane (the last partly, at D 96)
   constexpr int RS = kPartRow<D>;
   constexpr int R = kMergeRows;
   const int lane = threadIdx.x;
@@ -1085,7 +1086,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
         pm[r] = r < cn ? row[D] : -INFINITY;
         pl[r] = row[D + 1];
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) v[r][k] = row[lane + 64 * k];
+        for (int k = 0; k < DPL; ++k) v[r][k] = lane + 64 * k < D ? row[lane + 64 * k] : 0.f;
       }
       float cm = mx;
 #pragma unroll
@@ -1107,7 +1108,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
     const float inv = 1.f / (tot + 1e-6f);
     T* orow = out + ((int64_t)s * num_heads + h) * D + lane;
 #pragma unroll
-    for (int k = 0; k < DPL; ++k) store_from_f32<T>(orow + 64 * k, a[k] * inv);
+    for (int k = 0; k < DPL; ++k)
+      if (lane + 64 * k < D) store_from_f32<T>(orow + 64 * k, a[k] * inv);
   }
 }
 
@@ -1228,9 +1230,11 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (group == 2) return launch_decode_rows<T, D, BS, 2>(args...);   \
   if (group == 4) return launch_decode_rows<T, D, BS, 4>(args...);
 
-// 16-bit caches with head_dim 64 or 128 use the rows kernel; f32 and the
-// other head dims the generic kernel (head_dim 96 at 16-bit needs blocks of
-// 16 or 32 tokens: a (block, head) tile is a whole number of 1 KiB wave loads).
+// 16-bit caches use the rows kernel wherever a (block, head) tile is at
+// most 8 KiB, i.e. 8 wave loads per lane (rows_kernel_shape); f32 and the
+// two larger 16-bit tiles (head dims 192 and 256 at 32-token blocks) the
+// generic kernel. (Head dim 96 at 16-bit needs blocks of 16 or 32 tokens: a
+// tile is a whole number of 1 KiB wave loads.)
 #define VPA_DECODE_DBS16(T)                                   \
   if (D == 64 && BS == 8) { VPA_DECODE_ROWS_G(T, 64, 8) }     \
   if (D == 64 && BS == 16) { VPA_DECODE_ROWS_G(T, 64, 16) }   \
@@ -1238,13 +1242,13 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (D == 128 && BS == 8) { VPA_DECODE_ROWS_G(T, 128, 8) }   \
   if (D == 128 && BS == 16) { VPA_DECODE_ROWS_G(T, 128, 16) } \
   if (D == 128 && BS == 32) { VPA_DECODE_ROWS_G(T, 128, 32) } \
-  if (D == 96 && BS == 16) { VPA_DECODE_G(T, 96, 16) }        \
-  if (D == 96 && BS == 32) { VPA_DECODE_G(T, 96, 32) }        \
-  if (D == 192 && BS == 8) { VPA_DECODE_G(T, 192, 8) }        \
-  if (D == 192 && BS == 16) { VPA_DECODE_G(T, 192, 16) }      \
+  if (D == 96 && BS == 16) { VPA_DECODE_ROWS_G(T, 96, 16) }   \
+  if (D == 96 && BS == 32) { VPA_DECODE_ROWS_G(T, 96, 32) }   \
+  if (D == 192 && BS == 8) { VPA_DECODE_ROWS_G(T, 192, 8) }   \
+  if (D == 192 && BS == 16) { VPA_DECODE_ROWS_G(T, 192, 16) } \
   if (D == 192 && BS == 32) { VPA_DECODE_G(T, 192, 32) }      \
-  if (D == 256 && BS == 8) { VPA_DECODE_G(T, 256, 8) }        \
-  if (D == 256 && BS == 16) { VPA_DECODE_G(T, 256, 16) }      \
+  if (D == 256 && BS == 8) { VPA_DECODE_ROWS_G(T, 256, 8) }   \
+  if (D == 256 && BS == 16) { VPA_DECODE_ROWS_G(T, 256, 16) } \
   if (D == 256 && BS == 32) { VPA_DECODE_G(T, 256, 32) }
 
 #define VPA_DECODE_DBS(T)                                   \
@@ -1269,12 +1273,19 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (group == 2) return launch_decode_rows_fp8<T, D, BS, 2>(args...);   \
   if (group == 4) return launch_decode_rows_fp8<T, D, BS, 4>(args...);
 
+// fp8 shapes (decode_fp8_shape): a whole number of 1 KiB wave loads per
+// (block, head) tile, on the shapes whose 16-bit decode uses the rows kernel
+// too (the work list is the same for every cache type).
 #define VPA_DECODE_FP8_DBS(T)                                  \
   if (D == 64 && BS == 16) { VPA_DECODE_FP8_G(T, 64, 16) }     \
   if (D == 64 && BS == 32) { VPA_DECODE_FP8_G(T, 64, 32) }     \
   if (D == 128 && BS == 16) { VPA_DECODE_FP8_G(T, 128, 16) }   \
   if (D == 128 && BS == 32) { VPA_DECODE_FP8_G(T, 128, 32) }   \
-  if (D == 128 && BS == 8) { VPA_DECODE_FP8_G(T, 128, 8) }
+  if (D == 128 && BS == 8) { VPA_DECODE_FP8_G(T, 128, 8) }     \
+  if (D == 96 && BS == 32) { VPA_DECODE_FP8_G(T, 96, 32) }     \
+  if (D == 192 && BS == 16) { VPA_DECODE_FP8_G(T, 192, 16) }   \
+  if (D == 256 && BS == 8) { VPA_DECODE_FP8_G(T, 256, 8) }     \
+  if (D == 256 && BS == 16) { VPA_DECODE_FP8_G(T, 256, 16) }
 
 // fp8 caches: the rows kernel for bf16 / f16 queries.
 template <typename... A>
@@ -1419,7 +1430,7 @@ hipError_t launch_paged_read(int cache_dtype, const void* key_cache, const void*
 hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t max_context_len,
                               int32_t block_table_stride, int32_t num_seqs, const CacheGeom& g,
                               const DecodeWorkspace& ws, hipStream_t stream) {
-  const bool rows = decode_uses_rows_kernel(dtype, g.head_dim);
+  const bool rows = decode_uses_rows_kernel(dtype, g.head_dim, g.block_size);
   if (!rows || num_seqs == 0) return hipSuccess;
   hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, context_lens, num_seqs,
                      max_context_len, block_table_stride * g.block_size, kDecodeChunk, ws.items,
@@ -1450,14 +1461,24 @@ int fused_append_max_seqs() {
 
 bool decode_fuses_append(int dtype, int cache_dtype, int head_dim, int block_size,
                          int num_seqs, int group) {
-  return cache_dtype == dtype && decode_uses_rows_kernel(dtype, head_dim) &&
+  return cache_dtype == dtype && decode_uses_rows_kernel(dtype, head_dim, block_size) &&
          fused_append_shape(head_dim, block_size) && num_seqs <= fused_append_max_seqs() &&
          decode_kernel_group(group) == group;
 }
 
-bool decode_uses_rows_kernel(int dtype, int head_dim) {
-  return (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16) &&
-         (head_dim == 64 || head_dim == 128);
+bool decode_uses_rows_kernel(int dtype, int head_dim, int block_size) {
+  if (!(dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16)) return false;
+  if (!cache_kernels_supported(dtype, head_dim, block_size)) return false;
+  const int units = head_dim * block_size / 8;  // 16-byte units of a 16-bit tile
+  return units % 64 == 0 && units / 64 <= 8;
+}
+
+bool decode_fp8_shape(int head_dim, int block_size) {
+  if (!cache_kernels_supported(VPA_DTYPE_FP8_E4M3, head_dim, block_size)) return false;
+  if (!decode_uses_rows_kernel(VPA_DTYPE_BF16, head_dim, block_size)) return false;
+  // a whole number of 1 KiB loads per fp8 tile (at 8-token blocks a value
+  // unit holds two dims: head dims 128 and 256)
+  return block_size == 8 ? head_dim % 128 == 0 : (head_dim * block_size / 16) % 64 == 0;
 }
 
 namespace {
@@ -1485,8 +1506,8 @@ WorkspacePlan plan_workspace(int num_seqs, int num_heads, int head_dim, int max_
 }
 }  // namespace
 
-int decode_part_tokens(int dtype, int head_dim) {
-  return decode_uses_rows_kernel(dtype, head_dim) ? kDecodeChunk : kPT;
+int decode_part_tokens(int dtype, int head_dim, int block_size) {
+  return decode_uses_rows_kernel(dtype, head_dim, block_size) ? kDecodeChunk : kPT;
 }
 
 size_t decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_context_len,

@@ -64,7 +64,7 @@ struct DecodeAppend {
 // environment variable VPA_FUSED_APPEND_MAX_SEQS, read once, overrides it).
 constexpr int kFusedAppendMaxSeqs = 48;
 // True when vpa_reshape_and_cache_paged_attention runs its append inside the
-// decode launch (16-bit cache of the query's type, head_dim 64 / 128 with a
+// decode launch (16-bit cache of the query's type on the rows kernel with a
 // (block, head) tile of at least 2 KiB, at most kFusedAppendMaxSeqs sequences).
 bool decode_fuses_append(int dtype, int cache_dtype, int head_dim, int block_size,
                          int num_seqs, int group);
@@ -110,7 +110,7 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
 // Split-K partition (tokens) of the decode kernel that runs for a query
 // dtype and head_dim: the rows kernel's chunk, or the generic kernel's
 // partition.
-int decode_part_tokens(int dtype, int head_dim);
+int decode_part_tokens(int dtype, int head_dim, int block_size);
 // Decode scratch bytes and layout for partitions of part_tokens tokens; the
 // caller workspace of vpa_paged_attention uses kDecodeMinPartitionTokens
 // (valid for every kernel), the library's own scratch the running kernel's
@@ -247,9 +247,15 @@ hipError_t launch_paged_read(int cache_dtype, const void* key_cache, const void*
 // True when a decode kernel is compiled for this (dtype, head_dim, block_size,
 // query heads per kv head) combination.
 bool decode_supported(int dtype, int head_dim, int block_size, int group);
-// 16-bit caches at head_dim 64 and 128 decode with the rows kernel (and its
-// work list); every other shape with the generic split-K kernel.
-bool decode_uses_rows_kernel(int dtype, int head_dim);
+// 16-bit queries decode with the rows kernel (and its work list) where a
+// 16-bit (block, head) tile is 1 to 8 whole KiB (head dims 64 and 128, 96
+// at 16- and 32-token blocks, 192 and 256 at 8 and 16); f32 and the other
+// shapes with the generic split-K kernel. The work list depends on this
+// choice only, so it is the same for every cache type.
+bool decode_uses_rows_kernel(int dtype, int head_dim, int block_size);
+// fp8 caches decode on the rows kernel: head dims 64 and 128 at 16- and
+// 32-token blocks, 128 at 8, 96 at 32, 192 at 16, 256 at 8 and 16.
+bool decode_fp8_shape(int head_dim, int block_size);
 bool cache_kernels_supported(int dtype, int head_dim, int block_size);
 
 }  // namespace vpa

@@ -349,10 +349,24 @@ def test_reshape_and_cache_fp8_accepts_every_float_input(dtype):
     (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES),
      _lib.VPA_ERR_UNSUPPORTED, "differs"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bs=8, bstride=8 * 64 * 8, hstride=64 * 8),
-     _lib.VPA_ERR_UNSUPPORTED, "block_size 8"),
-    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bstride=8 * 256 * 16, hstride=256 * 16),
-     _lib.VPA_ERR_UNSUPPORTED, "head_dim 64 or 128"),
+     _lib.VPA_ERR_UNSUPPORTED, "(got 64, 8)"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bs=32, bstride=8 * 256 * 32, hstride=256 * 32),
+     _lib.VPA_ERR_UNSUPPORTED, "(got 256, 32)"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=192, bs=32, bstride=8 * 192 * 32, hstride=192 * 32),
+     _lib.VPA_ERR_UNSUPPORTED, "(got 192, 32)"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=96, bs=16, bstride=8 * 96 * 16, hstride=96 * 16),
+     _lib.VPA_ERR_UNSUPPORTED, "(got 96, 16)"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES), _lib.VPA_ERR_WORKSPACE, "workspace"),
+    # head dims 96 / 192 / 256 on the rows kernel: validation passes up to
+    # the workspace check
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=96, bs=32, bstride=8 * 96 * 32, hstride=96 * 32),
+     _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=192, bs=16, bstride=8 * 192 * 16, hstride=192 * 16),
+     _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bs=8, bts=128, bstride=8 * 256 * 8,
+          hstride=256 * 8), _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bs=16, bstride=8 * 256 * 16, hstride=256 * 16),
+     _lib.VPA_ERR_WORKSPACE, "workspace"),
 ])
 def test_paged_attention_fp8_validation(over, code, needle):
     rc, msg = pa_call(**over)

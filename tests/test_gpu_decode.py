@@ -193,7 +193,8 @@ def test_decode_chunk_boundaries_other_groups(device, h, kvh):
 @pytest.mark.parametrize("code,d,h,kvh,bs", [
     (orc.F32, 128, 16, 8, 16), (orc.BF16, 128, 16, 8, 16), (orc.F16, 128, 16, 8, 16),
     (orc.F32, 256, 16, 4, 16), (orc.F32, 192, 8, 2, 16), (orc.F32, 64, 16, 8, 8),
-    (orc.BF16, 128, 16, 8, 32), (orc.F16, 128, 16, 8, 8)])
+    (orc.BF16, 128, 16, 8, 32), (orc.F16, 128, 16, 8, 8), (orc.BF16, 256, 16, 4, 16),
+    (orc.F16, 96, 16, 8, 32)])
 def test_decode_large_logit_scales(device, factor, code, d, h, kvh, bs):
     got, want = decode_case(device, code, h, kvh, d, bs, CHUNK_EDGES, seed=300 + int(factor) + code,
                             scale=factor * d ** -0.5)
@@ -213,6 +214,20 @@ def test_decode_query_heads_per_kv_head(device, h, kvh, code, d, bs):
     lens = [1, 17, 511, 512, 2049, 4097]
     got, want = decode_case(device, code, h, kvh, d, bs, lens, seed=h + kvh + d + bs + code)
     assert_attention_close(got, want, code, f"h={h} kvh={kvh} code={code} d={d} bs={bs}")
+
+
+@pytest.mark.parametrize("d,bs,code", [(96, 16, orc.BF16), (96, 32, orc.F16), (192, 8, orc.BF16),
+                                       (192, 16, orc.F16), (256, 8, orc.F16),
+                                       (256, 16, orc.BF16)])
+@pytest.mark.parametrize("h,kvh", [(16, 8), (8, 8), (32, 4)])
+def test_decode_rows_kernel_head_dims(device, d, bs, code, h, kvh):
+    """Head dims 96, 192 and 256 on the rows kernel (16-bit tiles of 1.5 to 8
+    KiB: 3, 4, 6 or 8 wave loads per lane, stages of whole tiles) over the
+    wave and chunk edges, so partial rows of several chunks are merged
+    (head dim 96: 1.5 output elements per lane in the merge); 1, 2 and 8
+    query heads per kv head."""
+    got, want = decode_case(device, code, h, kvh, d, bs, CHUNK_EDGES, seed=d + bs + h + code)
+    assert_attention_close(got, want, code, f"rows d={d} bs={bs} h={h} kvh={kvh} code={code}")
 
 
 def test_decode_long_context_split_k(device):

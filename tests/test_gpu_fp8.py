@@ -203,6 +203,30 @@ def test_fp8_decode_head_dims_and_groups(device, d, h, kvh):
     assert_attention_close(got, want, orc.BF16, f"fp8 d={d} h={h} kvh={kvh}")
 
 
+# wave and chunk edges of the rows kernel (merges of 2 to 4 chunks)
+FP8_EDGES = [1, 7, 511, 512, 513, 2047, 2048, 2049, 4097, 6145]
+
+
+@pytest.mark.parametrize("d,bs", [(96, 32), (192, 16), (256, 8), (256, 16)])
+@pytest.mark.parametrize("code,scales,planned", [(orc.BF16, (1.0, 1.0), False),
+                                                 (orc.F16, (0.37, 3.1), True)])
+def test_fp8_decode_head_dims_96_192_256(device, d, bs, code, scales, planned):
+    """fp8 caches at head dims 96 (32-token blocks), 192 (16) and 256 (8 and
+    16; at 8 a value unit holds two dims of the block's 8 tokens), with and
+    without scales, planned and not, over the wave and chunk edges."""
+    got, want = fp8_decode_case(device, code, 16, 8, d, bs, FP8_EDGES, seed=d + bs + code,
+                                scales=scales, planned=planned)
+    assert_attention_close(got, want, code, f"fp8 d={d} bs={bs} code={code}")
+
+
+@pytest.mark.parametrize("d,bs", [(96, 32), (256, 16)])
+@pytest.mark.parametrize("h,kvh", [(8, 8), (16, 4), (64, 8)])
+def test_fp8_decode_head_dims_groups(device, d, bs, h, kvh):
+    got, want = fp8_decode_case(device, orc.BF16, h, kvh, d, bs, [3, 64, 300, 2500],
+                                seed=d + h + kvh + bs)
+    assert_attention_close(got, want, orc.BF16, f"fp8 d={d} bs={bs} h={h} kvh={kvh}")
+
+
 @pytest.mark.parametrize("planned", [False, True])
 @pytest.mark.parametrize("h,kvh", [(16, 8), (16, 4)])
 def test_fp8_decode_block_size_8(device, h, kvh, planned):

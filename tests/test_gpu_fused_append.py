@@ -104,7 +104,8 @@ EDGES = [1, 2, 15, 16, 17, 31, 32, 33, 511, 512, 513, 2047, 2048, 2049, 4097, 60
 
 
 @pytest.mark.parametrize("code", [orc.BF16, orc.F16])
-@pytest.mark.parametrize("d,bs", [(128, 16), (128, 8), (128, 32), (64, 16), (64, 8), (64, 32)])
+@pytest.mark.parametrize("d,bs", [(128, 16), (128, 8), (128, 32), (64, 16), (64, 8), (64, 32),
+                                  (96, 32), (192, 16), (256, 8), (256, 16)])
 @pytest.mark.parametrize("h,kvh", [(16, 8), (16, 4), (8, 8)])
 @pytest.mark.parametrize("planned", [False, True])
 def test_fused_equals_two_calls(device, code, d, bs, h, kvh, planned):
@@ -123,12 +124,14 @@ def test_fused_equals_two_calls(device, code, d, bs, h, kvh, planned):
 
 
 @pytest.mark.parametrize("what", ["bf16 batch 64", "f32", "fp8 cache", "head dim 96",
-                                  "head dim 256"])
+                                  "head dim 192"])
 def test_two_launch_form_equals_two_calls(device, what):
     """The configurations the one-launch form does not take (more than 48
-    sequences, f32 and fp8 caches, head dims other than 64 / 128) run the
-    append kernel on the slots derived from the tables, then the decode:
-    still the two calls' bytes and outputs."""
+    sequences, f32 and fp8 caches, 16-bit (block, head) tiles under 2 KiB,
+    as head dim 96 at 16-token blocks, and the shapes the rows kernel does
+    not take, as head dim 192 at 32) run the append kernel on the slots
+    derived from the tables, then the decode: still the two calls' bytes and
+    outputs."""
     rng = np.random.default_rng(sum(map(ord, what)))
     code, d, fp8, lens = orc.BF16, 128, False, EDGES
     if what == "bf16 batch 64":
@@ -139,13 +142,14 @@ def test_two_launch_form_equals_two_calls(device, what):
         fp8 = True
     else:
         d = int(what.split()[-1])
-    c = case(rng, code, 16, 8, d, 16, lens, fp8=fp8)
+    bs = 32 if d == 192 else 16
+    c = case(rng, code, 16, 8, d, bs, lens, fp8=fp8)
     if fp8:
         c["k_scale"], c["v_scale"] = 0.7, 1.9
     max_ctx = int(c["lens"].max())
     for planned in (False, True):
         got, gk, gv = fused(device, c, code, max_ctx, d ** -0.5, planned=planned)
-        want, wk, wv = two_calls(device, c, code, 16, max_ctx, d ** -0.5)
+        want, wk, wv = two_calls(device, c, code, bs, max_ctx, d ** -0.5)
         np.testing.assert_array_equal(gk, wk)
         np.testing.assert_array_equal(gv, wv)
         np.testing.assert_array_equal(got, want)
