@@ -265,7 +265,7 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
                 (double)softcapping);
   const bool fp8 = cache_dtype == VPA_DTYPE_FP8_E4M3;
   if (dtype != cache_dtype &&
-      !(fp8 && (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16)))
+      !(fp8 && (dtype == VPA_DTYPE_BF16 || dtype == VPA_DTYPE_F16 || dtype == VPA_DTYPE_F32)))
     return fail(VPA_ERR_UNSUPPORTED, "%s: cache dtype %s differs from query dtype %s", op,
                 dtype_name(cache_dtype), dtype_name(dtype));
   int rc = check_cache(op, cache_dtype, num_kv_heads, head_dim, block_size, num_blocks,
@@ -273,10 +273,15 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
   if (rc != VPA_OK) return rc;
   rc = check_scales(op, cache_dtype, k_scale, v_scale);
   if (rc != VPA_OK) return rc;
-  if (fp8 && !decode_fp8_shape(head_dim, block_size))
+  if (fp8 && dtype != VPA_DTYPE_F32 && !decode_fp8_shape(head_dim, block_size))
     return fail(VPA_ERR_UNSUPPORTED,
                 "%s: fp8 cache needs head_dim 64 or 128 with block_size 16 or 32, 128 or 256 "
                 "with 8, 96 with 32, 192 or 256 with 16 (got %d, %d)",
+                op, head_dim, block_size);
+  if (fp8 && dtype == VPA_DTYPE_F32 && !decode_f32_fp8_shape(head_dim, block_size))
+    return fail(VPA_ERR_UNSUPPORTED,
+                "%s: fp8 cache under f32 queries needs block_size 16 or 32 and a whole number "
+                "of 1 KiB wave loads per (block, head) tile (got head_dim %d, block_size %d)",
                 op, head_dim, block_size);
   if (num_seqs < 0 || num_heads <= 0 || max_context_len < 0 || block_table_stride < 0)
     return fail(VPA_ERR_INVALID_ARGUMENT,

@@ -80,32 +80,49 @@ __device__ __forceinline__ void tile_store(uint4* p, const uint4& v) {
   __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
 }
 
-template <typename T, int D, int BS, int G>
+// E4M3FN byte b (0..255) of an fp8 cache as f32 (exact, through gfx950's
+// conversion to bf16)
+__device__ __forceinline__ float fp8_elem_f32(uint32_t b) {
+  return bf16_bits_to_f32(fp8x2_to_pk<bf16_t>(b & 0xffu, false) & 0xffffu);
+}
+
+// C is the cache element type: T itself, or fp8_t under f32 queries (each
+// cache element read as f32(E4M3FN(byte) * scale), the product rounded to
+// f32, as the reference dequantises; a 16-byte vector then holds 16 dims of
+// a key or 16 tokens of a value row, and a lane's q chunk is 4 vectors).
+template <typename T, typename C, int D, int BS, int G>
 __global__ __launch_bounds__(64) void paged_decode_kernel(
-    T* __restrict__ out, const T* __restrict__ query, const T* __restrict__ key_cache,
-    const T* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
+    T* __restrict__ out, const T* __restrict__ query, const C* __restrict__ key_cache,
+    const C* __restrict__ value_cache, const uint32_t* __restrict__ block_tables,
     int32_t block_table_stride, const uint32_t* __restrict__ context_lens, int32_t max_ctx,
     float scale, int32_t num_heads, int64_t num_blocks, int64_t block_stride,
     int64_t head_stride, float* __restrict__ part_out, float* __restrict__ part_max,
-    float* __restrict__ part_sum, int32_t max_parts, int32_t kv_rep) {
-  constexpr int X = pack_x<T>();
+    float* __restrict__ part_sum, int32_t max_parts, int32_t kv_rep,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
+  constexpr bool kF8 = std::is_same_v<C, fp8_t>;
+  static_assert(std::is_same_v<C, T> || (kF8 && std::is_same_v<T, float>),
+                "cache type is the query type, or fp8 under f32 queries");
+  constexpr int X = pack_x<C>();
+  constexpr int QV = X * (int)sizeof(T) / 16;  // 16-byte q vectors per key chunk
   constexpr int LPT = 64 / BS;          // lanes per token in the key tile
   constexpr int KPL = D * BS / X / 64;  // key (and value) vectors per lane per block
   constexpr int VR = BS / X;            // vectors per value-tile row
   constexpr int DSTEP = 64 / VR;        // dim stride between a lane's value rows
   constexpr int PB = kPT / BS;          // blocks per partition
-  // Blocks whose loads are issued together: 16 vectors (64 VGPRs) in flight.
-  constexpr int kUnroll = KPL >= 16 ? 1 : (16 / KPL > 4 ? 4 : 16 / KPL);
+  // Blocks whose loads are issued together: 16 vectors (64 VGPRs) in flight
+  // (fp8: 4, whose 16 elements each are dequantised into registers)
+  constexpr int kVecs = kF8 ? 4 : 16;
+  constexpr int kUnroll = KPL >= kVecs ? 1 : (kVecs / KPL > 4 ? 4 : kVecs / KPL);
   static_assert(KPL >= 1 && (D * BS / X) % 64 == 0, "tile must cover the wave");
   static_assert(PB <= 64, "block-table slice must fit one wave");
 
   __shared__ float s_p[G][kPT];
-  // Shapes whose query vectors would not fit registers (G x KPL > 16, e.g.
-  // f32 at head_dim 256 with 32-token blocks: 128 vectors per lane) read
-  // them from LDS at each use instead.
-  constexpr bool kQinLds = G * KPL > 16;
-  constexpr int CHQ = D / X;  // 16-byte chunks of a query row
-  __shared__ uint4 s_q[kQinLds ? G * CHQ : 1];
+  // Shapes whose query vectors would not fit registers (G x KPL x QV > 16,
+  // e.g. f32 at head_dim 256 with 32-token blocks: 128 vectors per lane)
+  // read them from LDS at each use instead.
+  constexpr bool kQinLds = G * KPL * QV > 16;
+  constexpr int CHQ = D / X;  // key chunks of a query row (QV vectors each)
+  __shared__ uint4 s_q[kQinLds ? G * CHQ * QV : 1];
 
   const int lane = threadIdx.x;
   const int j = blockIdx.x;  // kv head
@@ -134,14 +151,15 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
   const uint32_t my_bt = lane < nb ? bt_row[b_begin + lane] : 0u;
 
   // Query chunks this lane multiplies against in the key tile: chunk
-  // lane / BS + k * LPT of each head, in registers or (kQinLds) in LDS.
-  uint4 qv[kQinLds ? 1 : G][kQinLds ? 1 : KPL];
+  // lane / BS + k * LPT of each head (QV vectors each), in registers or
+  // (kQinLds) in LDS.
+  uint4 qv[kQinLds ? 1 : G][kQinLds ? 1 : KPL][kQinLds ? 1 : QV];
   const int c0 = lane / BS;
   if constexpr (kQinLds) {
-    for (int i = lane; i < G * CHQ; i += 64) {
-      const int g = i / CHQ, c = i - g * CHQ;
+    for (int i = lane; i < G * CHQ * QV; i += 64) {
+      const int g = i / (CHQ * QV), c = i - g * (CHQ * QV);
       s_q[i] = *reinterpret_cast<const uint4*>(query + ((int64_t)s * num_heads + j * G + g) * D +
-                                                c * X);
+                                                c * (16 / (int)sizeof(T)));
     }
     lds_wave_sync();
   } else {
@@ -150,13 +168,18 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
       const T* qrow = query + ((int64_t)s * num_heads + j * G + g) * D;
 #pragma unroll
       for (int k = 0; k < KPL; ++k)
-        qv[g][k] = *reinterpret_cast<const uint4*>(qrow + (c0 + k * LPT) * X);
+#pragma unroll
+        for (int h = 0; h < QV; ++h)
+          qv[g][k][h] = *reinterpret_cast<const uint4*>(qrow + (c0 + k * LPT) * X +
+                                                         h * (16 / (int)sizeof(T)));
     }
   }
-  auto qchunk = [&](int g, int k) -> uint4 {
-    if constexpr (kQinLds) return s_q[g * CHQ + c0 + k * LPT];
-    else return qv[g][k];
+  auto qchunk = [&](int g, int k, int h) -> uint4 {
+    if constexpr (kQinLds) return s_q[(g * CHQ + c0 + k * LPT) * QV + h];
+    else return qv[g][k][h];
   };
+  const float ks = kF8 ? *k_scale : 1.f;
+  const float vs = kF8 ? *v_scale : 1.f;
 
   // j counts kv_rep replicas of every kv head (kv_rep > 1: more query heads
   // per kv head than G), so its cache head is j / kv_rep
@@ -186,11 +209,38 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
       if (bi < nb) {
         const int tok = (b_begin + bi) * BS + my_tok;
         const bool valid = ok[u] && tok < L;
+        // fp8: each chunk's 16 key elements dequantised once for every head
+        float dots[kF8 ? G : 1];
+        if constexpr (kF8) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) dots[g] = 0.f;
+#pragma unroll
+          for (int k = 0; k < KPL; ++k) {
+            float kf[16];
+            const uint32_t w[4] = {kv[u][k].x, kv[u][k].y, kv[u][k].z, kv[u][k].w};
+#pragma unroll
+            for (int e = 0; e < 16; ++e) kf[e] = fp8_elem_f32(w[e / 4] >> (8 * (e % 4))) * ks;
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+              for (int h = 0; h < QV; ++h) {
+                const uint4 q4 = qchunk(g, k, h);
+                dots[g] = fmaf(__uint_as_float(q4.x), kf[4 * h + 0], dots[g]);
+                dots[g] = fmaf(__uint_as_float(q4.y), kf[4 * h + 1], dots[g]);
+                dots[g] = fmaf(__uint_as_float(q4.z), kf[4 * h + 2], dots[g]);
+                dots[g] = fmaf(__uint_as_float(q4.w), kf[4 * h + 3], dots[g]);
+              }
+          }
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           float acc = 0.f;
+          if constexpr (kF8) {
+            acc = dots[g];
+          } else {
 #pragma unroll
-          for (int k = 0; k < KPL; ++k) acc = dot16<T>(qchunk(g, k), kv[u][k], acc);
+            for (int k = 0; k < KPL; ++k) acc = dot16<T>(qchunk(g, k, 0), kv[u][k], acc);
+          }
           acc = wave_sum_range<BS, 32>(acc);
           const float logit = valid ? acc * scale : -INFINITY;
           if (lane < BS) s_p[g][bi * BS + lane] = logit;
@@ -249,18 +299,45 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
         // Tokens past the context in the last block: zero the values so stale
         // cache contents (even NaN bit patterns) cannot leak in.
         if (tok0 + X > L) {
+          using E = std::conditional_t<kF8, uint8_t, T>;
 #pragma unroll
           for (int k = 0; k < KPL; ++k) {
             union {
               uint4 v;
-              T e[X];
+              E e[X];
             } w;
             w.v = vv[u][k];
 #pragma unroll
             for (int e = 0; e < X; ++e)
-              if (tok0 + e >= L) w.e[e] = T{};
+              if (tok0 + e >= L) w.e[e] = E{};
             vv[u][k] = w.v;
           }
+        }
+        if constexpr (kF8) {
+          // each value row's 16 elements dequantised once for every head,
+          // against the segment's 16 probabilities of the head (from LDS)
+#pragma unroll
+          for (int k = 0; k < KPL; ++k) {
+            float vf[16];
+            const uint32_t w[4] = {vv[u][k].x, vv[u][k].y, vv[u][k].z, vv[u][k].w};
+#pragma unroll
+            for (int e = 0; e < 16; ++e) vf[e] = fp8_elem_f32(w[e / 4] >> (8 * (e % 4))) * vs;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const float4* pp = reinterpret_cast<const float4*>(&s_p[g][bi * BS + seg * X]);
+              float a = acc[g][k];
+#pragma unroll
+              for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 t4 = pp[q4];
+                a = fmaf(t4.x, vf[4 * q4], a);
+                a = fmaf(t4.y, vf[4 * q4 + 1], a);
+                a = fmaf(t4.z, vf[4 * q4 + 2], a);
+                a = fmaf(t4.w, vf[4 * q4 + 3], a);
+              }
+              acc[g][k] = a;
+            }
+          }
+          continue;
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -1198,19 +1275,19 @@ hipError_t launch_decode_rows_fp8(void* out, const void* q, const void* kc, cons
                                                   v_scale, nullptr);
 }
 
-template <typename T, int D, int BS, int G>
-hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void* vc,
-                           const uint32_t* bt, int32_t bts, const uint32_t* cl, int32_t max_ctx,
-                           float scale, int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
-                           const DecodeWorkspace& ws, hipStream_t stream, const float*,
-                           const float*, const DecodeAppend*) {
+template <typename T, typename C, int D, int BS, int G>
+hipError_t launch_decode_tc(void* out, const void* q, const void* kc, const void* vc,
+                            const uint32_t* bt, int32_t bts, const uint32_t* cl, int32_t max_ctx,
+                            float scale, int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
+                            const DecodeWorkspace& ws, hipStream_t stream, const float* k_scale,
+                            const float* v_scale, const DecodeAppend*) {
   const int max_parts = (max_ctx + kPT - 1) / kPT;
   dim3 grid((unsigned)g.num_kv_heads, (unsigned)num_seqs, (unsigned)(max_parts > 0 ? max_parts : 1));
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, BS, G>), grid, dim3(64), 0, stream,
-                     static_cast<T*>(out), static_cast<const T*>(q), static_cast<const T*>(kc),
-                     static_cast<const T*>(vc), bt, bts, cl, max_ctx, scale, num_heads,
+  hipLaunchKernelGGL((paged_decode_kernel<T, C, D, BS, G>), grid, dim3(64), 0, stream,
+                     static_cast<T*>(out), static_cast<const T*>(q), static_cast<const C*>(kc),
+                     static_cast<const C*>(vc), bt, bts, cl, max_ctx, scale, num_heads,
                      g.num_blocks, g.block_stride, g.head_stride, ws.part_out, ws.part_max,
-                     ws.part_sum, ws.max_parts, g.kv_rep);
+                     ws.part_sum, ws.max_parts, g.kv_rep, k_scale, v_scale);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_parts <= 1) return e;
   dim3 rgrid((unsigned)num_heads, (unsigned)num_seqs);
@@ -1218,6 +1295,27 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
                      static_cast<T*>(out), cl, max_ctx, bts, g.block_size, num_heads, ws.part_out,
                      ws.part_max, ws.part_sum, ws.max_parts, kPT);
   return hipGetLastError();
+}
+
+template <typename T, int D, int BS, int G>
+hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void* vc,
+                           const uint32_t* bt, int32_t bts, const uint32_t* cl, int32_t max_ctx,
+                           float scale, int32_t num_seqs, int32_t num_heads, const CacheGeom& g,
+                           const DecodeWorkspace& ws, hipStream_t stream, const float* k_scale,
+                           const float* v_scale, const DecodeAppend* app) {
+  return launch_decode_tc<T, T, D, BS, G>(out, q, kc, vc, bt, bts, cl, max_ctx, scale, num_seqs,
+                                          num_heads, g, ws, stream, k_scale, v_scale, app);
+}
+template <int D, int BS, int G>
+hipError_t launch_decode_f32_fp8(void* out, const void* q, const void* kc, const void* vc,
+                                 const uint32_t* bt, int32_t bts, const uint32_t* cl,
+                                 int32_t max_ctx, float scale, int32_t num_seqs,
+                                 int32_t num_heads, const CacheGeom& g, const DecodeWorkspace& ws,
+                                 hipStream_t stream, const float* k_scale, const float* v_scale,
+                                 const DecodeAppend* app) {
+  return launch_decode_tc<float, fp8_t, D, BS, G>(out, q, kc, vc, bt, bts, cl, max_ctx, scale,
+                                                  num_seqs, num_heads, g, ws, stream, k_scale,
+                                                  v_scale, app);
 }
 
 #define VPA_DECODE_G(T, D, BS)                                          \
@@ -1287,11 +1385,27 @@ hipError_t launch_decode_t(void* out, const void* q, const void* kc, const void*
   if (D == 256 && BS == 8) { VPA_DECODE_FP8_G(T, 256, 8) }     \
   if (D == 256 && BS == 16) { VPA_DECODE_FP8_G(T, 256, 16) }
 
-// fp8 caches: the rows kernel for bf16 / f16 queries.
+#define VPA_DECODE_F32_FP8_G(D, BS)                                       \
+  if (group == 1) return launch_decode_f32_fp8<D, BS, 1>(args...);        \
+  if (group == 2) return launch_decode_f32_fp8<D, BS, 2>(args...);        \
+  if (group == 4) return launch_decode_f32_fp8<D, BS, 4>(args...);
+
+// fp8 caches: the rows kernel for bf16 / f16 queries; f32 queries on the
+// generic split-K kernel (decode_f32_fp8_shape).
 template <typename... A>
 hipError_t dispatch_decode_fp8(int dtype, int D, int BS, int group, A... args) {
   if (dtype == VPA_DTYPE_BF16) { VPA_DECODE_FP8_DBS(bf16_t) }
   if (dtype == VPA_DTYPE_F16) { VPA_DECODE_FP8_DBS(f16_t) }
+  if (dtype == VPA_DTYPE_F32) {
+    if (D == 64 && BS == 16) { VPA_DECODE_F32_FP8_G(64, 16) }
+    if (D == 64 && BS == 32) { VPA_DECODE_F32_FP8_G(64, 32) }
+    if (D == 96 && BS == 32) { VPA_DECODE_F32_FP8_G(96, 32) }
+    if (D == 128 && BS == 16) { VPA_DECODE_F32_FP8_G(128, 16) }
+    if (D == 128 && BS == 32) { VPA_DECODE_F32_FP8_G(128, 32) }
+    if (D == 192 && BS == 16) { VPA_DECODE_F32_FP8_G(192, 16) }
+    if (D == 192 && BS == 32) { VPA_DECODE_F32_FP8_G(192, 32) }
+    if (D == 256 && BS == 16) { VPA_DECODE_F32_FP8_G(256, 16) }
+  }
   return hipErrorInvalidValue;
 }
 
@@ -1471,6 +1585,15 @@ bool decode_uses_rows_kernel(int dtype, int head_dim, int block_size) {
   if (!cache_kernels_supported(dtype, head_dim, block_size)) return false;
   const int units = head_dim * block_size / 8;  // 16-byte units of a 16-bit tile
   return units % 64 == 0 && units / 64 <= 8;
+}
+
+bool decode_f32_fp8_shape(int head_dim, int block_size) {
+  // (tiles of at most 6 KiB: the 8 KiB one, head dim 256 at 32-token
+  // blocks, would not fit the generic kernel's registers with its dequantised
+  // elements)
+  const int units = head_dim * block_size / 16;
+  return cache_kernels_supported(VPA_DTYPE_FP8_E4M3, head_dim, block_size) && block_size >= 16 &&
+         units % 64 == 0 && units / 64 <= 6;
 }
 
 bool decode_fp8_shape(int head_dim, int block_size) {

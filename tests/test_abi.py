@@ -346,8 +346,16 @@ def test_reshape_and_cache_fp8_accepts_every_float_input(dtype):
 
 @pytest.mark.parametrize("over,code,needle", [
     (dict(cdtype=FP8, **F8_STRIDES), _lib.VPA_ERR_INVALID_ARGUMENT, "k_scale and v_scale"),
+    # f32 queries over fp8 caches: the generic split-K kernel, tiles of up to
+    # 6 KiB at 16- and 32-token blocks
     (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES),
-     _lib.VPA_ERR_UNSUPPORTED, "differs"),
+     _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, d=192, bs=32,
+          bstride=8 * 192 * 32, hstride=192 * 32), _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bs=32,
+          bstride=8 * 256 * 32, hstride=256 * 32), _lib.VPA_ERR_UNSUPPORTED, "f32 queries"),
+    (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bts=128, bstride=8 * 128 * 8,
+          hstride=128 * 8), _lib.VPA_ERR_UNSUPPORTED, "f32 queries"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bs=8, bstride=8 * 64 * 8, hstride=64 * 8),
      _lib.VPA_ERR_UNSUPPORTED, "(got 64, 8)"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bs=32, bstride=8 * 256 * 32, hstride=256 * 32),

@@ -227,6 +227,25 @@ def test_fp8_decode_head_dims_groups(device, d, bs, h, kvh):
     assert_attention_close(got, want, orc.BF16, f"fp8 d={d} bs={bs} h={h} kvh={kvh}")
 
 
+@pytest.mark.parametrize("d,bs", [(64, 16), (96, 32), (128, 16), (128, 32), (192, 16),
+                                  (192, 32), (256, 16)])
+@pytest.mark.parametrize("scales,planned", [((1.0, 1.0), False), ((0.37, 3.1), True)])
+def test_fp8_decode_f32_queries(device, d, bs, scales, planned):
+    """f32 queries over fp8 caches (the generic split-K kernel: each element
+    read as f32(E4M3FN(byte) * scale), rel 1e-5 against the fp64 oracle's same
+    dequantisation) over the 128-token partitions and the merge of many."""
+    got, want = fp8_decode_case(device, orc.F32, 16, 8, d, bs, FP8_EDGES, seed=d + bs + 11,
+                                scales=scales, planned=planned)
+    assert_attention_close(got, want, orc.F32, f"f32/fp8 d={d} bs={bs} scales={scales}")
+
+
+@pytest.mark.parametrize("h,kvh", [(8, 8), (16, 4), (24, 8), (64, 8)])
+def test_fp8_decode_f32_queries_groups(device, h, kvh):
+    got, want = fp8_decode_case(device, orc.F32, h, kvh, 128, 16, [1, 5, 128, 129, 700, 3000],
+                                seed=h + kvh + 13, scales=(0.5, 2.0))
+    assert_attention_close(got, want, orc.F32, f"f32/fp8 h={h} kvh={kvh}")
+
+
 @pytest.mark.parametrize("planned", [False, True])
 @pytest.mark.parametrize("h,kvh", [(16, 8), (16, 4)])
 def test_fp8_decode_block_size_8(device, h, kvh, planned):
