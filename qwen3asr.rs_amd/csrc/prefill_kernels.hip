@@ -383,6 +383,9 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   const C* kbase = key_cache + (int64_t)j * head_stride;
   const C* vbase = value_cache + (int64_t)j * head_stride;
   const uint32_t* bt = block_tables + (int64_t)s * block_table_stride;
+  const char* kbytes = reinterpret_cast<const char*>(kbase);
+  const char* vbytes = reinterpret_cast<const char*>(vbase);
+  const uint64_t bstride_b = (uint64_t)block_stride * sizeof(C);  // bytes between blocks
   const int last_blk = max(k_len - 1, 0) / BS;
   // every u32 block id is inside the pool (the id checks compare 32 bits,
   // in scalar registers, otherwise)
@@ -408,12 +411,13 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   // its global base is uniform and each lane adds a fixed element offset:
   // K regions are plain copies of the block's [chunk][key] units, V regions
   // transpose the block's [dim][unit] rows to [unit][dim].
-  uint32_t koff[DPW], voff[DPW];
+  uint32_t koffb[DPW], voffb[DPW];  // bytes
 #pragma unroll
   for (int i = 0; i < DPW; ++i) {
     const int r = ((wave * DPW + i) % DPB) * 64 + lane;  // unit of the block region
-    koff[i] = (uint32_t)(r * X);
-    voff[i] = kPairRows ? (uint32_t)(r * X) : (uint32_t)((r % D) * BS + (r / D) * X);
+    koffb[i] = (uint32_t)(r * X) * (uint32_t)sizeof(C);
+    voffb[i] = (kPairRows ? (uint32_t)(r * X) : (uint32_t)((r % D) * BS + (r / D) * X)) *
+               (uint32_t)sizeof(C);
   }
 
   // Issue the DMAs of the SUB tiles of step t into stage S (always all SUB
@@ -421,10 +425,13 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   // absent blocks read block 0 (in bounds); they are masked in S and their
   // values zeroed when the V operands are built.
   // block ids of the SUB tiles of step t
-  // (with a table row of at least NB entries: one NB-dword scalar load of a
-  // window of the row that holds every entry the step needs, the window
-  // moved back from the sequence's tail so that it stays inside the row;
-  // entries past the last block repeat it, as the per-entry clamp does)
+  // (with a table row of at least NB entries: one NB-dword scalar load of the
+  // window of the row that starts at the step's first block, clamped to the
+  // sequence's last one. Entries past the last block are whatever the row
+  // holds there: their keys are masked and their DMAs read block 0. Only
+  // where the row ends inside the window are the entries loaded one by one,
+  // clamped to the last block. The load has no branch around it to merge
+  // with, so its wait lands at the ids' first use, a step later.)
   constexpr int NB = SUB * NBT;  // block ids of a step
   const bool wide_ids = block_table_stride >= NB;
   auto step_blocks = [&](int t, uint32_t (&pbs)[SUB][NBT]) {
@@ -433,27 +440,21 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
       for (int u = 0; u < SUB; ++u) tile_blocks((t * SUB + u) * KT, pbs[u]);
       return;
     }
-    const int first = __builtin_amdgcn_readfirstlane(t * SUB * KT / BS);
-    const int base = max(0, min(first, last_blk - (NB - 1)));
-    const uint32_t* p = bt + base;
+    const int first = __builtin_amdgcn_readfirstlane(min(t * SUB * KT / BS, last_blk));
+    const int base = min(first, block_table_stride - NB);
     uint32_t w[NB];
 #pragma unroll
-    for (int i = 0; i < NB; ++i) w[i] = p[i];
-    if (first + NB - 1 <= last_blk) {  // base == first
+    for (int i = 0; i < NB; ++i) w[i] = bt[base + i];
+    if (base != first) {  // rare: the table row ends inside the window
 #pragma unroll
-      for (int i = 0; i < NB; ++i) pbs[i / NBT][i % NBT] = w[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        const int k = min(first + i, last_blk) - base;
-        uint32_t id = w[0];
-#pragma unroll
-        for (int c = 1; c < NB; ++c) id = k == c ? w[c] : id;
-        pbs[i / NBT][i % NBT] = id;
-      }
+      for (int i = 0; i < NB; ++i) w[i] = bt[min(first + i, last_blk)];
     }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) pbs[i / NBT][i % NBT] = w[i];
   };
-  auto issue = [&](auto sc, int t, const uint32_t (&pbs)[SUB][NBT]) {
+  // (full: every block of the step inside the pool and every key inside the
+  // context, so the ids are used unchecked)
+  auto issue = [&](auto sc, auto full, int t, const uint32_t (&pbs)[SUB][NBT]) {
     if (DMW < kPrefillWaves && wave >= DMW) return;  // wave issues no DMA (uniform)
 #pragma unroll
     for (int u = 0; u < SUB; ++u) {
@@ -478,11 +479,18 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
           // indexed scratch array: load the id from the table instead)
           phys = bt[__builtin_amdgcn_readfirstlane(min(k0 / BS + b, last_blk))];
         }
-        phys = (k0 + b * BS < k_len && phys <= max_id) ? phys : 0u;
+        if constexpr (!decltype(full)::value)
+          phys = (k0 + b * BS < k_len && phys <= max_id) ? phys : 0u;
         phys = __builtin_amdgcn_readfirstlane(phys);
-        const int64_t blk = (int64_t)phys * block_stride;
-        dma16(kbase + blk + koff[i], sk + b * RBK + (di % DPB) * 64);
-        dma16(vbase + blk + voff[i], sv + b * RBV + (di % DPB) * 64);
+        // the block's byte offset in scalar registers (the compiler would
+        // otherwise fuse the multiply into a 64-bit vector multiply-add per
+        // DMA)
+        const uint64_t blk = (uint64_t)phys * bstride_b;
+        const uint64_t ub =
+            ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(blk >> 32)) << 32) |
+            __builtin_amdgcn_readfirstlane((uint32_t)blk);
+        dma16(kbytes + ub + koffb[i], sk + b * RBK + (di % DPB) * 64);
+        dma16(vbytes + ub + voffb[i], sv + b * RBV + (di % DPB) * 64);
       }
     }
   };
@@ -576,12 +584,12 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   // sum; O^T += V^T . P^T with P^T straight from the accumulator
   auto accumulate = [&](const uint4* sv, const f32x16_t& sacc, float m_use) {
     float sval[16];
-    float ps = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int r = 0; r < 16; ++r)
       sval[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], sl, -m_use));
-      ps += sval[r];
-    }
+    float ps = sval[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) ps += sval[r];
     lsum += ps;
     uint4 pk[2];
 #pragma unroll
@@ -676,8 +684,9 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   // steps: pi (step t + 1, for the DMAs issued here) was loaded one step
   // earlier and the ids of step t + 2 are loaded into pf here, so no step
   // waits for a table load; the masks of step t need only which of its
-  // blocks are inside the pool (pres, worked out when its DMAs were issued;
-  // pres_next gets step t + 1's).
+  // blocks are inside the pool (pres, worked out when its DMAs were issued,
+  // as "all of them" or 0 for "work the bits out"; pres_next gets step
+  // t + 1's).
   // (With four blocks per tile the DMAs load their block ids from the table
   // themselves and the registers of two steps' ids would not fit the larger
   // shapes: each step then loads its own ids, before its waits, for the
@@ -689,7 +698,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
     constexpr int S = decltype(sc)::value;
     const bool refill = t + 1 < n_steps;
     if constexpr (kCarryIds) {
-      if (t + 2 < n_steps) step_blocks(t + 2, pf);
+      step_blocks(t + 2, pf);  // (past the last step: loaded, not used)
     } else {
       uint32_t own[SUB][NBT];
       step_blocks(t, own);
@@ -714,6 +723,13 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
 #pragma unroll
       for (int u = 0; u < SUB; ++u) vmask[u] = 0xffffffffu;
     } else {
+      if constexpr (kCarryIds) {
+        if (pres != kAllPresent) {  // some block may be absent: the step's ids again
+          uint32_t own[SUB][NBT];
+          step_blocks(t, own);
+          pres = step_present(own);
+        }
+      }
 #pragma unroll
       for (int u = 0; u < SUB; ++u) {
         vmask[u] = tile_mask(t * SUB + u, (pres >> (u * NBT)) & ((1u << NBT) - 1u));
@@ -731,8 +747,23 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
       asm volatile("" ::: "memory");
     }
     if (refill) {
-      if constexpr (kCarryIds) pres_next = step_present(pi);
-      issue(Int<1 - S>{}, t + 1, pi);
+      if constexpr (kCarryIds) {
+        // only whether every block is in the pool is worked out ahead (a
+        // maximum over the ids); a step with an absent block reloads its ids
+        // for the bits
+        uint32_t mx = pi[0][0];
+#pragma unroll
+        for (int u = 0; u < SUB; ++u)
+#pragma unroll
+          for (int kb = 0; kb < NBT; ++kb) mx = max(mx, pi[u][kb]);
+        pres_next = mx <= max_id ? kAllPresent : 0u;
+        if (pres_next == kAllPresent && (t + 2) * (SUB * KT) <= k_len)
+          issue(Int<1 - S>{}, std::true_type{}, t + 1, pi);
+        else
+          issue(Int<1 - S>{}, std::false_type{}, t + 1, pi);
+      } else {
+        issue(Int<1 - S>{}, std::false_type{}, t + 1, pi);
+      }
     }
     compute(sc, t, vmask);
   };
@@ -743,7 +774,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
     uint32_t p0 = 0, p1 = 0;
     step_blocks(0, ix);
     p0 = step_present(ix);
-    issue(Int<0>{}, 0, ix);
+    issue(Int<0>{}, std::false_type{}, 0, ix);
     if (kCarryIds && 1 < n_steps) step_blocks(1, ix);
     for (int t0 = 0; t0 < n_steps; t0 += 2) {
       step(Int<0>{}, t0, p0, ix, iy, p1);      // loads the ids of t0 + 2 into iy
