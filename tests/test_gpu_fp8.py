@@ -395,6 +395,19 @@ def test_fp8_prefill_absent_block_in_either_tile_of_a_step(device, col):
     assert_attention_close(got, want, orc.BF16, f"fp8 prefill absent column {col}")
 
 
+@pytest.mark.parametrize("col", [17, 29])
+def test_fp8_prefill_absent_block_in_a_later_step(device, col):
+    """Four-tile steps of 8 blocks: an absent block in step 2 (column 17) or
+    step 3 (column 29), whose ids come from the window loaded two steps
+    ahead; the step works its mask out from its ids loaded again."""
+    def mutate(bt):
+        bt[0, col] = 1 << 30
+    got, want, _ = fp8_prefill_case(device, orc.BF16, 16, 8, 16, [500, 60], [40, 50],
+                                    seed=50 + col, mutate_bt=mutate)
+    assert np.isfinite(got).all()
+    assert_attention_close(got, want, orc.BF16, f"fp8 prefill absent column {col}")
+
+
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("bs", [16, 32])
 def test_fp8_prefill_head_dim_64(device, bs, causal):

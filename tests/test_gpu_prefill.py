@@ -176,6 +176,20 @@ def test_prefill_absent_block_in_either_tile_of_a_step(device, col):
     assert_attention_close(got, want, orc.BF16, f"absent column {col}")
 
 
+@pytest.mark.parametrize("col", [9, 13])
+def test_prefill_absent_block_in_a_later_step(device, col):
+    """Steps 2 and later take their block ids from the window loaded two
+    steps ahead and learn only whether every block is in the pool; a step
+    with an absent block (column 9: step 2, column 13: step 3) works its
+    mask out from its ids loaded again."""
+    def mutate(bt):
+        bt[0, col] = 1 << 30
+    got, want = prefill_case(device, orc.BF16, 16, 8, 128, 16, [200, 60], [40, 50],
+                             seed=20 + col, stale_nan=True, mutate_bt=mutate)
+    assert np.isfinite(got).all()
+    assert_attention_close(got, want, orc.BF16, f"absent column {col}")
+
+
 def test_prefill_padded_table_columns_and_frozen_maxima(device):
     """Extra zero columns in block_tables and host maxima above the true ones
     (a grid sized for a larger batch) change nothing."""
