@@ -316,11 +316,28 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   const int s = rest / q_tiles;
   const int qt = q_tiles - 1 - rest % q_tiles;
 
+  // The block ids of the first two steps are the first 2 NB0 entries of the
+  // table row: loaded here, alongside the sequence's lengths, not after them
+  // (up to 4 ids per step: more would not fit the scalar registers of the
+  // larger shapes)
+  constexpr int NB0 = prefill_step_tiles<kF8, D, BS>() * (kPrefillKeys / BS);
+  constexpr bool kEarly = NB0 <= 4;
+  const bool early_ids = kEarly && block_table_stride >= 2 * NB0;
+  uint32_t w01[kEarly ? 2 * NB0 : 1];
+  if (early_ids) {
+    const uint32_t* row0 = block_tables + (int64_t)s * block_table_stride;
+#pragma unroll
+    for (int i = 0; i < 2 * NB0; ++i) w01[i] = row0[i];
+  }
   const uint32_t qa = cu_seqlens_q[s], qb = cu_seqlens_q[s + 1];
+  const uint32_t ctx = context_lens[s];
+  // (all of them in flight together: a load the compiler would sink to its
+  // first use, past the early exit, would wait on its own)
+  asm volatile("" ::"s"(qa), "s"(qb), "s"(ctx));
   int q_len = qb > qa ? (int)min(qb - qa, (uint32_t)max_query_len) : 0;
   if ((int64_t)qa >= total_query_rows) q_len = 0;
   else q_len = (int)min((int64_t)q_len, total_query_rows - (int64_t)qa);
-  const int k_len = (int)min(context_lens[s], (uint32_t)max_kv_len);
+  const int k_len = (int)min(ctx, (uint32_t)max_kv_len);
 
   const int p0 = qt * PPB;
   if (p0 >= q_len) return;  // whole workgroup: tile past this sequence's queries
@@ -353,10 +370,12 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
   }
   uint4 qop[KS];
   {
-    const T* qrow = query + (row * num_heads + head) * D + 8 * half;
+    // (every lane loads: a row past the sequence's queries reads its first
+    // row instead, in bounds, so the loads need no branch; such a row's
+    // scores and output stay in its own lane and column and are not stored)
+    const T* qrow = query + ((row_ok ? row : (int64_t)qa) * num_heads + head) * D + 8 * half;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qop[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks) : make_uint4(0, 0, 0, 0);
+    for (int ks = 0; ks < KS; ++ks) qop[ks] = *reinterpret_cast<const uint4*>(qrow + 16 * ks);
     // a negative scale is folded into Q (a sign flip, exact in the cache
     // type), so the row max can be taken on the raw scores
     if (scale_log2 < 0.f) {
@@ -772,10 +791,24 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_eu<D>()))) void prefill_pag
     // and of the one after it; presence bits of the current and next step
     uint32_t ix[SUB][NBT] = {}, iy[SUB][NBT] = {};
     uint32_t p0 = 0, p1 = 0;
-    step_blocks(0, ix);
+    // ids of step t in {0, 1}: entries t NB0 .. t NB0 + NB0 - 1 of the row
+    // (entries past the sequence's last block are never dereferenced: their
+    // keys lie past the context, so their DMAs read block 0 and their keys
+    // are masked)
+    auto early_blocks = [&](int t, uint32_t (&pbs)[SUB][NBT]) {
+      if constexpr (kEarly) {
+#pragma unroll
+        for (int i = 0; i < NB0; ++i) pbs[i / NBT][i % NBT] = w01[t * NB0 + i];
+      }
+    };
+    if (early_ids) early_blocks(0, ix);
+    else step_blocks(0, ix);
     p0 = step_present(ix);
     issue(Int<0>{}, std::false_type{}, 0, ix);
-    if (kCarryIds && 1 < n_steps) step_blocks(1, ix);
+    if (kCarryIds && 1 < n_steps) {
+      if (early_ids) early_blocks(1, ix);
+      else step_blocks(1, ix);
+    }
     for (int t0 = 0; t0 < n_steps; t0 += 2) {
       step(Int<0>{}, t0, p0, ix, iy, p1);      // loads the ids of t0 + 2 into iy
       step(Int<1>{}, t0 + 1, p1, iy, ix, p0);  // loads the ids of t0 + 3 into ix
