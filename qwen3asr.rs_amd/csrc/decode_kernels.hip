@@ -116,7 +116,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
   static_assert(KPL >= 1 && (D * BS / X) % 64 == 0, "tile must cover the wave");
   static_assert(PB <= 64, "block-table slice must fit one wave");
 
-  __shared__ float s_p[G][kPT];
+  __shared__ __align__(16) float s_p[G][kPT];  // (rows read as float4 by the fp8 value pass)
   // Shapes whose query vectors would not fit registers (G x KPL x QV > 16,
   // e.g. f32 at head_dim 256 with 32-token blocks: 128 vectors per lane)
   // read them from LDS at each use instead.
