@@ -489,6 +489,29 @@ def test_argmax_oracle_nan_and_infinity_rule():
     np.testing.assert_array_equal(orc.argmax_rows(x), [0, 2, 0, 0, 2])
 
 
+def test_argmax_oracle_nan_rows_against_nanargmax():
+    """Rows with NaN scattered in them (and ties, infinities): the scan's rule
+    is numpy's nanargmax (the first maximum of the non-NaN elements), except
+    that a NaN in element 0 is kept (nothing compares greater than it)."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((200, 300)).astype(np.float32)
+    for r in range(200):
+        x[r, rng.choice(300, size=rng.integers(1, 60), replace=False)] = np.nan
+        if r % 5 == 0:
+            x[r, rng.choice(300, size=3, replace=False)] = np.inf
+        if r % 7 == 0:
+            x[r, 0] = np.nan
+        if r % 11 == 0:  # ties of the row's maximum
+            m = np.nanmax(x[r])
+            x[r, rng.choice(300, size=2, replace=False)] = m
+    want = np.array([0 if np.isnan(row[0]) else np.nanargmax(row) for row in x])
+    np.testing.assert_array_equal(orc.argmax_rows(x), want)
+    xb = orc.from_f32(x, orc.BF16)
+    xf = orc.to_f32(xb, orc.BF16)
+    want_b = np.array([0 if np.isnan(row[0]) else np.nanargmax(row) for row in xf])
+    np.testing.assert_array_equal(orc.argmax_rows(xb, dtype=orc.BF16), want_b)
+
+
 def _reference_decode_loop(pending, steps_logits_ids, eos_ids):
     """The reference's host loop (paged_batch_engine.rs:640-667 and :722):
     active rows are compacted; a pending EOS id finishes its row, others are
