@@ -13,7 +13,8 @@
   bf16/f16 tolerance 2e-2, with stale NaN bytes past each context;
 * chunked prefill over an fp8 cache: the fp64 oracle (causal and not,
   scales, absent blocks, NaN bytes in every unused slot), and with scales 1
-  bit-equal to the bf16 kernel over a bf16 copy of the cache.
+  bit-equal to the bf16 kernel over a bf16 copy of the cache (also at c4's
+  full size).
 """
 
 import numpy as np
@@ -581,3 +582,36 @@ def test_fp8_append_slot_patterns(device, t, pattern):
     orc.reshape_and_cache_fp8(k, v, kc, vc, slots, orc.BF16, 0.5, 2.0)
     np.testing.assert_array_equal(f8_host(kcd), kc)
     np.testing.assert_array_equal(f8_host(vcd), vc)
+
+
+def test_fp8_prefill_c4_equals_bf16_prefill_over_dequantised_cache(device):
+    """c4 at full size (64 sequences x 512 new tokens over 62..1008 prior
+    ones, 5502-block pool): with scales 1 the fp8 kernel's output equals, bit
+    for bit, the bf16 kernel's over a bf16 copy of the cache (E4M3 values
+    are exact in bf16, and both kernels share their softmax groups)."""
+    from vpa import workloads
+    w = workloads.c4()
+    code, h, kvh, d, bs = orc.BF16, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    nb = w.num_blocks
+    rng = np.random.default_rng(w.seed + 1)
+    kc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d // 16, bs, 16)) * 2)
+                          .astype(np.float32))
+    vc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d, bs)) * 2).astype(np.float32))
+    tq = int(w.query_lens.sum())
+    q = to_dev(random_words(rng, (tq, h, d), code), code, device)
+    bt, lens, cu = u32(w.block_tables, device), u32(w.context_lens, device), u32(w.cu_seqlens_q, device)
+    one = scalar(1.0, device)
+    mq, mk = int(w.query_lens.max()), int(w.context_lens.max())
+    got = vpa.paged_attention_varlen_prefill(q, f8(kc, device), f8(vc, device), bt, lens, cu,
+                                             one, one, d ** -0.5, 1.0, causal=True,
+                                             max_query_len=mq, max_context_len=mk)
+    kf = orc.fp8_to_f32(kc).transpose(0, 1, 3, 2, 4).reshape(nb, kvh, bs, d)
+    kb = orc.from_f32(np.ascontiguousarray(
+        kf.reshape(nb, kvh, bs, d // 8, 8).transpose(0, 1, 3, 2, 4)), code)
+    vb = orc.from_f32(orc.fp8_to_f32(vc), code)
+    ref = vpa.paged_attention_varlen_prefill(q, to_dev(kb, code, device), to_dev(vb, code, device),
+                                             bt, lens, cu, None, None, d ** -0.5, 1.0,
+                                             causal=True, max_query_len=mq, max_context_len=mk)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert torch.isfinite(got.float()).all()
