@@ -285,7 +285,12 @@ int vpa_reshape_and_cache_paged_attention_planned(
  * fit returns VPA_ERR_WORKSPACE (after the other argument checks, before
  * touching the device). Same arguments (minus the workspace), results and
  * errors as vpa_paged_attention. Every call on a GPU shares that GPU's
- * array: calls that overlap on one GPU (several streams or threads) race.
+ * array. Calls outside stream capture are ordered one after another on each
+ * GPU (each call's stream waits for an event recorded after the previous
+ * call, on whatever stream): several streams or threads do not race, their
+ * calls serialise. Calls captured into a HIP graph are not ordered by the
+ * library: the graph's replays must not overlap another use of the array on
+ * that GPU.
  */
 int vpa_paged_attention_noalloc(void* out, const void* query, const float* k_scale,
                                 const float* v_scale, const void* key_cache,

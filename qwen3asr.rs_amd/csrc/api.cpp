@@ -382,6 +382,12 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
   // then the decode: the same bytes and results either way.
   const bool fuse = append != nullptr &&
                     decode_fuses_append(dtype, cache_dtype, head_dim, block_size, num_seqs, group);
+  // the library's scratch orders the calls that share it
+  if (scratch != nullptr) {
+    const int rc_b = scratch->before(op, stream);
+    if (rc_b != VPA_OK) return rc_b;
+  }
+  int rc_l = VPA_OK;
   if (append != nullptr && !fuse) {
     LastSlots last;
     last.block_tables = block_tables;
@@ -393,14 +399,16 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
         dtype, cache_dtype, append->key, append->value, append->key_token_stride,
         append->value_token_stride, const_cast<void*>(key_cache), const_cast<void*>(value_cache),
         last, num_seqs, g, k_scale, v_scale, static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return hip_status(op, e);
+    if (e != hipSuccess) rc_l = hip_status(op, e);
   }
-  return hip_status(op, launch_paged_decode(dtype, cache_dtype, out, query, key_cache,
+  if (rc_l == VPA_OK)
+    rc_l = hip_status(op, launch_paged_decode(dtype, cache_dtype, out, query, key_cache,
                                             value_cache, block_tables, block_table_stride,
                                             context_lens, max_context_len, softmax_scale,
                                             k_scale, v_scale, num_seqs, num_heads, g, ws,
                                             static_cast<hipStream_t>(stream),
                                             fuse ? append : nullptr));
+  return scratch != nullptr ? scratch->after(op, stream, rc_l) : rc_l;
 }
 
 }  // namespace vpa

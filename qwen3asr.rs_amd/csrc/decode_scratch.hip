@@ -11,8 +11,13 @@
 // than the caller workspace of vpa_paged_attention (sized for any kernel).
 // Nothing in it needs to start at zero: the plan launch rewrites the work
 // list and its header, and every partial row the merge reads is written by
-// the same call first. Every call on a GPU shares that GPU's array, so
-// calls that overlap on one GPU (two streams, two threads) race.
+// the same call first. Every call on a GPU shares that GPU's array. Calls
+// outside stream capture are ordered one after another on each GPU: each
+// call's stream first waits for an event recorded after the previous call
+// (whatever stream that was on), so two streams or two threads do not race
+// on the array. Calls captured into a graph are not ordered by the library
+// (a graph cannot wait for an event recorded outside it): replays must not
+// overlap another use of the array on that GPU.
 
 #include <atomic>
 #include <mutex>
@@ -41,6 +46,60 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch[kMaxDevices];
 std::mutex g_scratch_mu;
+
+// Per GPU: an event recorded after the last call outside stream capture,
+// which the next call's stream waits for (created at the first such call on
+// that GPU). g_order_mu is held from a call's wait through its record.
+std::mutex g_order_mu;
+hipEvent_t g_done[kMaxDevices];
+bool g_have_done[kMaxDevices];
+thread_local int t_order_dev = -1;  // the device of this thread's ordered call
+
+// Before a call's launches: outside stream capture, take the order lock and
+// make the stream wait for the previous call on this GPU.
+int order_before(const char* op, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(st, &cs);
+  if (e != hipSuccess)
+    return fail(VPA_ERR_HIP, "%s: hipStreamIsCapturing failed: %s", op, hipGetErrorString(e));
+  t_order_dev = -1;
+  if (cs != hipStreamCaptureStatusNone) return VPA_OK;  // replays ordered by the caller
+  int dev = -1;
+  e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(VPA_ERR_HIP, "%s: hipGetDevice failed: %s", op, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(VPA_ERR_UNSUPPORTED, "%s: device ordinal %d out of range", op, dev);
+  g_order_mu.lock();
+  if (g_have_done[dev]) {
+    e = hipStreamWaitEvent(st, g_done[dev], 0);
+    if (e != hipSuccess) {
+      g_order_mu.unlock();
+      return fail(VPA_ERR_HIP, "%s: hipStreamWaitEvent failed: %s", op, hipGetErrorString(e));
+    }
+  }
+  t_order_dev = dev;
+  return VPA_OK;
+}
+
+// After the launches: record this call's event and release the order lock.
+int order_after(const char* op, void* stream, int rc) {
+  const int dev = t_order_dev;
+  if (dev < 0) return rc;  // captured
+  t_order_dev = -1;
+  hipError_t e = hipSuccess;
+  if (rc == VPA_OK && !g_have_done[dev]) {
+    e = hipEventCreateWithFlags(&g_done[dev], hipEventDisableTiming);
+    if (e == hipSuccess) g_have_done[dev] = true;
+  }
+  if (rc == VPA_OK && e == hipSuccess)
+    e = hipEventRecord(g_done[dev], static_cast<hipStream_t>(stream));
+  g_order_mu.unlock();
+  if (rc == VPA_OK && e != hipSuccess)
+    return fail(VPA_ERR_HIP, "%s: ordering event failed: %s", op, hipGetErrorString(e));
+  return rc;
+}
 
 // Device address of the current device's copy of `scratch`, looked up once
 // per device with that device current.
@@ -92,7 +151,8 @@ int vpa_paged_attention_noalloc(void* out, const void* query, const float* k_sca
                                 int32_t head_dim, int32_t block_size, int64_t num_blocks,
                                 int64_t cache_block_stride, int64_t cache_head_stride,
                                 int32_t dtype, int32_t cache_dtype, void* stream) {
-  static const DecodeScratch kScratch{kScratchBytes, scratch_address};
+  static const DecodeScratch kScratch{kScratchBytes, scratch_address, order_before,
+                                      order_after};
   return paged_attention_impl(out, query, k_scale, v_scale, key_cache, value_cache, block_tables,
                               block_table_stride, context_lens, alibi_slopes, max_context_len,
                               softmax_scale, softcapping, sinks, num_seqs, num_heads,

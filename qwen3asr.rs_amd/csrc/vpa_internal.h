@@ -80,6 +80,11 @@ int device_cu_count();
 struct DecodeScratch {
   size_t bytes;
   int (*address)(const char* op, void** out);
+  // Called after every argument check, right before the call's launches on
+  // `stream` (VPA_OK or an error status, then nothing is launched), and
+  // after them with their status (returns the call's status).
+  int (*before)(const char* op, void* stream);
+  int (*after)(const char* op, void* stream, int rc);
 };
 
 // Bytes of the static decode scratch on each GPU (VPA_NOALLOC_SCRATCH_MIB).

@@ -101,3 +101,36 @@ def test_noalloc_equals_workspace_entry_point_twice(device, code, cache_code):
                               dtype=code, kv_dtype=orc.FP8 if cache_code == orc.FP8 else None)
     assert_attention_close(orc.to_f32(got, code), ref, code, "noalloc second call")
 
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(device):
+    """A large call on one stream and a small one on another, issued back to
+    back with no synchronisation between them, both on the one scratch array:
+    each equals the workspace entry point's result (the library makes the
+    second call's stream wait for the first call)."""
+    lib = _lib.load()
+    rng = np.random.default_rng(77)
+    big = [int(x) for x in rng.integers(2000, 4500, size=256)]
+    small = [int(x) for x in rng.integers(1000, 3000, size=16)]
+    cases = [case(rng, orc.BF16, big), case(rng, orc.BF16, small)]
+    want = [call(device, c, orc.BF16, orc.BF16, False, int(max(c["lens"]))) for c in cases]
+    args = []
+    for c in cases:
+        q = to_dev(c["q"], orc.BF16, device)
+        kc, vc = dev_cache(c["kc"], orc.BF16, device), dev_cache(c["vc"], orc.BF16, device)
+        bt, lens = u32(c["bt"], device), u32(c["lens"], device)
+        out = torch.full_like(q, float("nan"))
+        args.append((out, q, kc, vc, bt, lens, c))
+    streams = [torch.cuda.Stream(device), torch.cuda.Stream(device)]
+    torch.cuda.synchronize()
+    for (out, q, kc, vc, bt, lens, c), st in zip(args, streams):
+        b = len(c["lens"])
+        rc = lib.vpa_paged_attention_noalloc(
+            out.data_ptr(), q.data_ptr(), None, None, kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
+            bt.shape[1], lens.data_ptr(), None, int(max(c["lens"])), D ** -0.5, 1.0, None, b, H,
+            KVH, D, BS, c["nb"], kc.stride(0), kc.stride(1), _lib.DTYPE_BF16, _lib.DTYPE_BF16,
+            st.cuda_stream)
+        assert rc == 0, lib.vpa_last_error().decode()
+    torch.cuda.synchronize()
+    for (out, *_), w in zip(args, want):
+        assert np.array_equal(to_host(out), w), "a call on the other stream changed the result"
