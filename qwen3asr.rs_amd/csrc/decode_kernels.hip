@@ -354,7 +354,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
               a = fmaf(p4.w, __uint_as_float(v.w), a);
               acc[g][k] = a;
             }
-          } else {
+          } else if constexpr (!kF8) {
             // 16-bit caches: probabilities rounded to the cache type, pairs
             // of tokens per v_dot2.
             const float4 pa = *reinterpret_cast<const float4*>(pp);
