@@ -12,13 +12,18 @@ times the default logit scale the f32 and f16 paths drew elements up to 1.5
 times the element-wise bound while their error stayed at 1e-6 (f32) and
 1e-3 (f16) of the output's largest magnitude, the types' own rounding
 against the fp64 oracle. The same acceptance tolerances as the per-op tests
-(tests/_util.assert_attention_close)."""
+(tests/_util.assert_attention_close). A wider sweep adds f32 queries over
+fp8 caches, prefill over f32 and fp8 caches with the denominator's epsilon,
+every prefill head dim and block size, the fp8 decode shapes of each query
+type and 3 to 8 query heads per kv head; f32 queries over fp8 caches are
+held to rel 1e-5 per output row there (normwise), their near-zero elements
+being the rounding of cancelling terms."""
 
 import numpy as np
 import pytest
 
 from oracle import oracle as orc
-from tests._util import assert_attention_close
+from tests._util import assert_attention_close, assert_attention_close_normwise
 from tests.test_gpu_decode import decode_case
 from tests.test_gpu_fp8 import fp8_decode_case
 from tests.test_gpu_prefill import prefill_case
@@ -94,3 +99,60 @@ def test_fp8_decode_random_shape(device, case):
     assert_attention_close(got, want, code,
                            f"case {case}: code={code} d={d} bs={bs} h={h} kvh={kvh} "
                            f"lens={lens} scales={scales}")
+
+
+# Query types f32 / bf16 / f16 over f32 / 16-bit / fp8 caches, query heads
+# per kv head 1-8 (3 and 6 included), every prefill head dim and block size,
+# and the fp8 decode shapes the library takes for its query type.
+_FP8_DECODE_16 = [(64, 16), (64, 32), (128, 8), (128, 16), (128, 32), (256, 8), (96, 32),
+                  (192, 16), (256, 16)]
+_FP8_DECODE_F32 = [(d, bs) for d in (64, 96, 128, 192, 256) for bs in (16, 32)
+                   if (d * bs // 16) % 64 == 0 and (d * bs // 16) // 64 <= 6]
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_wide_random_shape(device, case):
+    from tests.test_gpu_prefill_vector import vector_case
+    rng = np.random.default_rng(11000 + case)
+    op = ["decode", "prefill", "fp8_decode", "fp8_prefill"][case % 4]
+    code = int(rng.choice([orc.F32, orc.BF16, orc.F16]))
+    g = int(rng.choice([1, 2, 3, 4, 6, 8]))
+    kvh = int(rng.choice([1, 2, 4, 8]))
+    h = g * kvh
+    what = f"case {case}: {op} code={code} h={h} kvh={kvh}"
+    if op in ("decode", "fp8_decode"):
+        lens = _lens(rng, int(rng.integers(1, 9)), 3000)
+        if op == "decode":
+            d, bs = _shape(rng, code)
+            scale = float(rng.uniform(0.5, 1.5)) * d ** -0.5
+            got, want = decode_case(device, code, h, kvh, d, bs, lens, seed=12000 + case,
+                                    scale=scale)
+        else:
+            opts = _FP8_DECODE_F32 if code == orc.F32 else _FP8_DECODE_16
+            d, bs = opts[int(rng.integers(0, len(opts)))]
+            scales = (float(rng.uniform(0.3, 1.5)), float(rng.uniform(0.2, 3.0)))
+            got, want = fp8_decode_case(device, code, h, kvh, d, bs, lens, seed=12000 + case,
+                                        scales=scales)
+        what += f" d={d} bs={bs} lens={lens}"
+    else:
+        d = int(rng.choice([64, 96, 128, 192, 256]))
+        bs = int(rng.choice([8, 16, 32]))
+        n = int(rng.integers(1, 5))
+        prior = [int(v) for v in rng.integers(0, 600, size=n)]
+        new = _lens(rng, n, 300)
+        causal = bool(rng.integers(0, 2))
+        eps = float(rng.choice([0.0, 1e-6]))
+        scale = float(rng.uniform(0.5, 1.5)) * d ** -0.5
+        fp8 = op == "fp8_prefill"
+        scales = (float(rng.uniform(0.3, 1.5)), float(rng.uniform(0.2, 3.0))) if fp8 else (1.0, 1.0)
+        got, want = vector_case(device, code, h, kvh, d, bs, prior, new, seed=12000 + case,
+                                causal=causal, eps=eps, fp8=fp8, scales=scales, scale=scale)
+        what += f" d={d} bs={bs} prior={prior} new={new} causal={causal} eps={eps}"
+    if code == orc.F32 and op.startswith("fp8"):
+        # f32 queries over fp8 values (normal x 2, then v_scale up to 3):
+        # outputs near zero come from cancelling terms several times larger,
+        # whose f32 sums over thousands of tokens sit at up to ~2x the
+        # element-wise bound; the rows are held to rel 1e-5 normwise
+        assert_attention_close_normwise(got, want, code, what)
+    else:
+        assert_attention_close(got, want, code, what)
