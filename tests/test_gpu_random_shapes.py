@@ -15,9 +15,10 @@ against the fp64 oracle. The same acceptance tolerances as the per-op tests
 (tests/_util.assert_attention_close). A wider sweep adds f32 queries over
 fp8 caches, prefill over f32 and fp8 caches with the denominator's epsilon,
 every prefill head dim and block size, the fp8 decode shapes of each query
-type and 3 to 8 query heads per kv head; f32 queries over fp8 caches are
-held to rel 1e-5 per output row there (normwise), their near-zero elements
-being the rounding of cancelling terms."""
+type and 3 to 8 query heads per kv head; fp8 caches under f32 or bf16
+queries are held to the tolerance per output row there (normwise): with
+scales other than 1 the reference rounds each dequantised element to the
+query type, the kernels scale in f32."""
 
 import numpy as np
 import pytest
@@ -110,7 +111,7 @@ _FP8_DECODE_F32 = [(d, bs) for d in (64, 96, 128, 192, 256) for bs in (16, 32)
                    if (d * bs // 16) % 64 == 0 and (d * bs // 16) // 64 <= 6]
 
 
-@pytest.mark.parametrize("case", range(24))
+@pytest.mark.parametrize("case", range(64))
 def test_wide_random_shape(device, case):
     from tests.test_gpu_prefill_vector import vector_case
     rng = np.random.default_rng(11000 + case)
@@ -148,11 +149,14 @@ def test_wide_random_shape(device, case):
         got, want = vector_case(device, code, h, kvh, d, bs, prior, new, seed=12000 + case,
                                 causal=causal, eps=eps, fp8=fp8, scales=scales, scale=scale)
         what += f" d={d} bs={bs} prior={prior} new={new} causal={causal} eps={eps}"
-    if code == orc.F32 and op.startswith("fp8"):
-        # f32 queries over fp8 values (normal x 2, then v_scale up to 3):
-        # outputs near zero come from cancelling terms several times larger,
-        # whose f32 sums over thousands of tokens sit at up to ~2x the
-        # element-wise bound; the rows are held to rel 1e-5 normwise
+    if op.startswith("fp8") and code in (orc.F32, orc.BF16):
+        # fp8 with scales other than 1: the kernels scale the logits and the
+        # output in f32 where the reference (and the oracle) rounds each
+        # dequantised element to the query type first; with bf16 queries
+        # that rounding, and with f32 queries the cancelling f32 sums over
+        # thousands of tokens, put outputs near zero at up to ~2.6x the
+        # element-wise bound (errors below 1 % of the output's largest
+        # magnitude): the rows are held to the tolerance normwise
         assert_attention_close_normwise(got, want, code, what)
     else:
         assert_attention_close(got, want, code, what)
