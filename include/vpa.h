@@ -290,7 +290,8 @@ int vpa_reshape_and_cache_paged_attention_planned(
  * call, on whatever stream): several streams or threads do not race, their
  * calls serialise. Calls captured into a HIP graph are not ordered by the
  * library: the graph's replays must not overlap another use of the array on
- * that GPU.
+ * that GPU. The array's address and the ordering event are set up at the
+ * first call on each GPU; no later call creates or allocates anything.
  */
 int vpa_paged_attention_noalloc(void* out, const void* query, const float* k_scale,
                                 const float* v_scale, const void* key_cache,

@@ -48,11 +48,14 @@ std::atomic<void*> g_scratch[kMaxDevices];
 std::mutex g_scratch_mu;
 
 // Per GPU: an event recorded after the last call outside stream capture,
-// which the next call's stream waits for (created at the first such call on
-// that GPU). g_order_mu is held from a call's wait through its record.
+// which the next call's stream waits for. It is created with the lookup of
+// the scratch's address (the set-up at the first call on that GPU), so no
+// later call creates anything. g_order_mu is held from a call's wait
+// through its record.
 std::mutex g_order_mu;
 hipEvent_t g_done[kMaxDevices];
-bool g_have_done[kMaxDevices];
+std::atomic<bool> g_done_ready[kMaxDevices];
+bool g_recorded[kMaxDevices];
 thread_local int t_order_dev = -1;  // the device of this thread's ordered call
 
 // Before a call's launches: outside stream capture, take the order lock and
@@ -71,8 +74,9 @@ int order_before(const char* op, void* stream) {
     return fail(VPA_ERR_HIP, "%s: hipGetDevice failed: %s", op, hipGetErrorString(e));
   if (dev < 0 || dev >= kMaxDevices)
     return fail(VPA_ERR_UNSUPPORTED, "%s: device ordinal %d out of range", op, dev);
+  if (!g_done_ready[dev].load(std::memory_order_acquire)) return VPA_OK;  // no scratch in use
   g_order_mu.lock();
-  if (g_have_done[dev]) {
+  if (g_recorded[dev]) {
     e = hipStreamWaitEvent(st, g_done[dev], 0);
     if (e != hipSuccess) {
       g_order_mu.unlock();
@@ -89,12 +93,10 @@ int order_after(const char* op, void* stream, int rc) {
   if (dev < 0) return rc;  // captured
   t_order_dev = -1;
   hipError_t e = hipSuccess;
-  if (rc == VPA_OK && !g_have_done[dev]) {
-    e = hipEventCreateWithFlags(&g_done[dev], hipEventDisableTiming);
-    if (e == hipSuccess) g_have_done[dev] = true;
-  }
-  if (rc == VPA_OK && e == hipSuccess)
+  if (rc == VPA_OK) {
     e = hipEventRecord(g_done[dev], static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) g_recorded[dev] = true;
+  }
   g_order_mu.unlock();
   if (rc == VPA_OK && e != hipSuccess)
     return fail(VPA_ERR_HIP, "%s: ordering event failed: %s", op, hipGetErrorString(e));
@@ -119,6 +121,11 @@ int scratch_address(const char* op, void** out) {
       if (e != hipSuccess || p == nullptr)
         return fail(VPA_ERR_HIP, "%s: hipGetSymbolAddress of the decode scratch failed: %s", op,
                     hipGetErrorString(e));
+      e = hipEventCreateWithFlags(&g_done[dev], hipEventDisableTiming);
+      if (e != hipSuccess)
+        return fail(VPA_ERR_HIP, "%s: hipEventCreateWithFlags failed: %s", op,
+                    hipGetErrorString(e));
+      g_done_ready[dev].store(true, std::memory_order_release);
       g_scratch[dev].store(p, std::memory_order_release);
     }
   }
