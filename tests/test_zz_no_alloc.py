@@ -7,7 +7,8 @@ smaller batch and shorter contexts so that it runs over what the first left
 in the array. The second call is also checked against the fp64 oracle.
 Covered: the rows kernel with multi-chunk sequences (bf16, merge launch),
 the fp8-cache rows kernel, and the generic kernel (f32, 256-token
-partitions). The rejection of a call larger than the scratch happens on the
+partitions); calls on two streams; the call captured in a HIP graph and
+replayed. The rejection of a call larger than the scratch happens on the
 host before any device access and is tested in the CPU suite
 (tests/test_abi.py), where no GPU exists for a wrong launch to reach."""
 
@@ -134,3 +135,53 @@ def test_noalloc_calls_on_two_streams_are_ordered(device):
     torch.cuda.synchronize()
     for (out, *_), w in zip(args, want):
         assert np.array_equal(to_host(out), w), "a call on the other stream changed the result"
+
+
+def test_noalloc_captured_in_a_graph_matches_eager(device):
+    """The allocation-free decode recorded in a HIP graph (what the entry
+    point is for: it makes no allocation under capture), replayed four
+    times with new queries and longer contexts copied into the captured
+    buffers, eager work and synchronisation between replays: every replay
+    equals the workspace entry point run eagerly on the same inputs, bit for
+    bit, and the last one the fp64 oracle."""
+    lib = _lib.load()
+    rng = np.random.default_rng(53)
+    lens0 = np.array([int(x) for x in rng.integers(1, 3000, size=24)])
+    lens0[:3] = [2047, 2048, 4000]  # multi-chunk rows at the later steps: the merge launch
+    max_ctx = 4096
+    c = case(rng, orc.BF16, [max_ctx] * len(lens0))
+    b = len(lens0)
+    q = to_dev(c["q"], orc.BF16, device)
+    kc, vc = dev_cache(c["kc"], orc.BF16, device), dev_cache(c["vc"], orc.BF16, device)
+    bt = u32(c["bt"], device)
+    lens = u32(lens0.astype(np.uint32), device)
+    out = torch.full_like(q, float("nan"))
+
+    def decode(stream):
+        rc = lib.vpa_paged_attention_noalloc(
+            out.data_ptr(), q.data_ptr(), None, None, kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
+            bt.shape[1], lens.data_ptr(), None, max_ctx, D ** -0.5, 1.0, None, b, H, KVH, D, BS,
+            c["nb"], kc.stride(0), kc.stride(1), _lib.DTYPE_BF16, _lib.DTYPE_BF16, stream)
+        assert rc == 0, lib.vpa_last_error().decode()
+
+    decode(torch.cuda.current_stream(device).cuda_stream)  # set-up and warm-up, before capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        decode(torch.cuda.current_stream(device).cuda_stream)
+    torch.cuda.synchronize()
+    for t in range(1, 5):
+        c["q"] = random_words(rng, (b, H, D), orc.BF16)
+        c["lens"] = np.minimum(lens0 + 37 * t, max_ctx).astype(np.uint32)
+        q.copy_(to_dev(c["q"], orc.BF16, device))
+        lens.copy_(u32(c["lens"], device))
+        want = call(device, c, orc.BF16, orc.BF16, False, max_ctx)  # eager, with a workspace
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = to_host(out)
+        assert np.array_equal(got, want), f"replay {t} differs from the eager call"
+    ref = orc.paged_attention(c["q"], c["kc"], c["vc"], c["bt"], c["lens"], max_ctx, D ** -0.5,
+                              dtype=orc.BF16)
+    assert_attention_close(orc.to_f32(got, orc.BF16), ref, orc.BF16, "noalloc graph replay")
