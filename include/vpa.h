@@ -153,7 +153,7 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * divide G) replicas of each kv head, each reading that head's tiles.
  * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 with a bf16 or f16
  * query (head_dim 64 or 128 with block_size 16 or 32, 128 or 256 with 8,
- * 96 with 32, 192 or 256 with 16) or an f32 query (block_size 16 or 32,
+ * 96 with 32, 192 or 256 with 16 or 32) or an f32 query (block_size 16 or 32,
  * tiles of at most 6 KiB: every head_dim but 96 at 16 tokens and 256 at 32):
  * K and V are then read as
  * (float)byte * (*k_scale) and (float)byte * (*v_scale), k_scale / v_scale

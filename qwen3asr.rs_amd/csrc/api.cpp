@@ -276,7 +276,7 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
   if (fp8 && dtype != VPA_DTYPE_F32 && !decode_fp8_shape(head_dim, block_size))
     return fail(VPA_ERR_UNSUPPORTED,
                 "%s: fp8 cache needs head_dim 64 or 128 with block_size 16 or 32, 128 or 256 "
-                "with 8, 96 with 32, 192 or 256 with 16 (got %d, %d)",
+                "with 8, 96 with 32, 192 or 256 with 16 or 32 (got %d, %d)",
                 op, head_dim, block_size);
   if (fp8 && dtype == VPA_DTYPE_F32 && !decode_f32_fp8_shape(head_dim, block_size))
     return fail(VPA_ERR_UNSUPPORTED,

@@ -86,10 +86,12 @@ __device__ __forceinline__ float fp8_elem_f32(uint32_t b) {
   return bf16_bits_to_f32(fp8x2_to_pk<bf16_t>(b & 0xffu, false) & 0xffffu);
 }
 
-// C is the cache element type: T itself, or fp8_t under f32 queries (each
-// cache element read as f32(E4M3FN(byte) * scale), the product rounded to
-// f32, as the reference dequantises; a 16-byte vector then holds 16 dims of
-// a key or 16 tokens of a value row, and a lane's q chunk is 4 vectors).
+// C is the cache element type: T itself, or fp8_t (each cache element read
+// as f32(E4M3FN(byte) * scale) rounded to the query type, as the reference
+// dequantises; a 16-byte vector then holds 16 dims of a key or 16 tokens of
+// a value row, and a lane's q chunk is 4 vectors of f32 or 2 of 16 bits).
+// The fp8 instances under 16-bit queries serve the tiles the rows kernel
+// does not take (head dims 192 and 256 at 32-token blocks).
 template <typename T, typename C, int D, int BS, int G>
 __global__ __launch_bounds__(64) void paged_decode_kernel(
     T* __restrict__ out, const T* __restrict__ query, const C* __restrict__ key_cache,
@@ -100,8 +102,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
     float* __restrict__ part_sum, int32_t max_parts, int32_t kv_rep,
     const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
   constexpr bool kF8 = std::is_same_v<C, fp8_t>;
-  static_assert(std::is_same_v<C, T> || (kF8 && std::is_same_v<T, float>),
-                "cache type is the query type, or fp8 under f32 queries");
+  static_assert(std::is_same_v<C, T> || kF8, "cache type is the query type, or fp8");
   constexpr int X = pack_x<C>();
   constexpr int QV = X * (int)sizeof(T) / 16;  // 16-byte q vectors per key chunk
   constexpr int LPT = 64 / BS;          // lanes per token in the key tile
@@ -220,16 +221,30 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
             const uint32_t w[4] = {kv[u][k].x, kv[u][k].y, kv[u][k].z, kv[u][k].w};
 #pragma unroll
             for (int e = 0; e < 16; ++e) kf[e] = fp8_elem_f32(w[e / 4] >> (8 * (e % 4))) * ks;
+            if constexpr (std::is_same_v<T, float>) {
 #pragma unroll
-            for (int g = 0; g < G; ++g)
+              for (int g = 0; g < G; ++g)
 #pragma unroll
-              for (int h = 0; h < QV; ++h) {
-                const uint4 q4 = qchunk(g, k, h);
-                dots[g] = fmaf(__uint_as_float(q4.x), kf[4 * h + 0], dots[g]);
-                dots[g] = fmaf(__uint_as_float(q4.y), kf[4 * h + 1], dots[g]);
-                dots[g] = fmaf(__uint_as_float(q4.z), kf[4 * h + 2], dots[g]);
-                dots[g] = fmaf(__uint_as_float(q4.w), kf[4 * h + 3], dots[g]);
-              }
+                for (int h = 0; h < QV; ++h) {
+                  const uint4 q4 = qchunk(g, k, h);
+                  dots[g] = fmaf(__uint_as_float(q4.x), kf[4 * h + 0], dots[g]);
+                  dots[g] = fmaf(__uint_as_float(q4.y), kf[4 * h + 1], dots[g]);
+                  dots[g] = fmaf(__uint_as_float(q4.z), kf[4 * h + 2], dots[g]);
+                  dots[g] = fmaf(__uint_as_float(q4.w), kf[4 * h + 3], dots[g]);
+                }
+            } else {
+              // the elements rounded to the query type, pairs per v_dot2
+              uint4 kq[2];
+#pragma unroll
+              for (int h = 0; h < 2; ++h)
+                kq[h] = make_uint4(pack2_hw<T>(kf[8 * h + 0], kf[8 * h + 1]),
+                                   pack2_hw<T>(kf[8 * h + 2], kf[8 * h + 3]),
+                                   pack2_hw<T>(kf[8 * h + 4], kf[8 * h + 5]),
+                                   pack2_hw<T>(kf[8 * h + 6], kf[8 * h + 7]));
+#pragma unroll
+              for (int g = 0; g < G; ++g)
+                dots[g] = dot16<T>(qchunk(g, k, 1), kq[1], dot16<T>(qchunk(g, k, 0), kq[0], dots[g]));
+            }
           }
         }
 #pragma unroll
@@ -322,19 +337,44 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
             const uint32_t w[4] = {vv[u][k].x, vv[u][k].y, vv[u][k].z, vv[u][k].w};
 #pragma unroll
             for (int e = 0; e < 16; ++e) vf[e] = fp8_elem_f32(w[e / 4] >> (8 * (e % 4))) * vs;
+            if constexpr (std::is_same_v<T, float>) {
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-              const float4* pp = reinterpret_cast<const float4*>(&s_p[g][bi * BS + seg * X]);
-              float a = acc[g][k];
+              for (int g = 0; g < G; ++g) {
+                const float4* pp = reinterpret_cast<const float4*>(&s_p[g][bi * BS + seg * X]);
+                float a = acc[g][k];
 #pragma unroll
-              for (int q4 = 0; q4 < 4; ++q4) {
-                const float4 t4 = pp[q4];
-                a = fmaf(t4.x, vf[4 * q4], a);
-                a = fmaf(t4.y, vf[4 * q4 + 1], a);
-                a = fmaf(t4.z, vf[4 * q4 + 2], a);
-                a = fmaf(t4.w, vf[4 * q4 + 3], a);
+                for (int q4 = 0; q4 < 4; ++q4) {
+                  const float4 t4 = pp[q4];
+                  a = fmaf(t4.x, vf[4 * q4], a);
+                  a = fmaf(t4.y, vf[4 * q4 + 1], a);
+                  a = fmaf(t4.z, vf[4 * q4 + 2], a);
+                  a = fmaf(t4.w, vf[4 * q4 + 3], a);
+                }
+                acc[g][k] = a;
               }
-              acc[g][k] = a;
+            } else {
+              // values and probabilities rounded to the query type, token
+              // pairs per v_dot2
+              uint4 vq[2];
+#pragma unroll
+              for (int h = 0; h < 2; ++h)
+                vq[h] = make_uint4(pack2_hw<T>(vf[8 * h + 0], vf[8 * h + 1]),
+                                   pack2_hw<T>(vf[8 * h + 2], vf[8 * h + 3]),
+                                   pack2_hw<T>(vf[8 * h + 4], vf[8 * h + 5]),
+                                   pack2_hw<T>(vf[8 * h + 6], vf[8 * h + 7]));
+#pragma unroll
+              for (int g = 0; g < G; ++g) {
+                const float4* pp = reinterpret_cast<const float4*>(&s_p[g][bi * BS + seg * X]);
+                float a = acc[g][k];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                  const float4 pa = pp[2 * h], pb = pp[2 * h + 1];
+                  const uint4 pk = make_uint4(pack2_hw<T>(pa.x, pa.y), pack2_hw<T>(pa.z, pa.w),
+                                              pack2_hw<T>(pb.x, pb.y), pack2_hw<T>(pb.z, pb.w));
+                  a = dot16<T>(pk, vq[h], a);
+                }
+                acc[g][k] = a;
+              }
             }
           }
           continue;
@@ -1318,6 +1358,19 @@ hipError_t launch_decode_f32_fp8(void* out, const void* q, const void* kc, const
                                                   v_scale, app);
 }
 
+template <typename T, int D, int BS, int G>
+hipError_t launch_decode_generic_fp8(void* out, const void* q, const void* kc, const void* vc,
+                                     const uint32_t* bt, int32_t bts, const uint32_t* cl,
+                                     int32_t max_ctx, float scale, int32_t num_seqs,
+                                     int32_t num_heads, const CacheGeom& g,
+                                     const DecodeWorkspace& ws, hipStream_t stream,
+                                     const float* k_scale, const float* v_scale,
+                                     const DecodeAppend* app) {
+  return launch_decode_tc<T, fp8_t, D, BS, G>(out, q, kc, vc, bt, bts, cl, max_ctx, scale,
+                                              num_seqs, num_heads, g, ws, stream, k_scale,
+                                              v_scale, app);
+}
+
 #define VPA_DECODE_G(T, D, BS)                                          \
   if (group == 1) return launch_decode_t<T, D, BS, 1>(args...);         \
   if (group == 2) return launch_decode_t<T, D, BS, 2>(args...);         \
@@ -1371,9 +1424,16 @@ hipError_t launch_decode_f32_fp8(void* out, const void* q, const void* kc, const
   if (group == 2) return launch_decode_rows_fp8<T, D, BS, 2>(args...);   \
   if (group == 4) return launch_decode_rows_fp8<T, D, BS, 4>(args...);
 
+#define VPA_DECODE_GENERIC_FP8_G(T, D, BS)                                    \
+  if (group == 1) return launch_decode_generic_fp8<T, D, BS, 1>(args...);     \
+  if (group == 2) return launch_decode_generic_fp8<T, D, BS, 2>(args...);     \
+  if (group == 4) return launch_decode_generic_fp8<T, D, BS, 4>(args...);
+
 // fp8 shapes (decode_fp8_shape): a whole number of 1 KiB wave loads per
-// (block, head) tile, on the shapes whose 16-bit decode uses the rows kernel
-// too (the work list is the same for every cache type).
+// (block, head) tile, on the rows kernel where the 16-bit decode of the
+// shape uses it too (the work list is the same for every cache type), on
+// the generic kernel where it does not (head dims 192 and 256 at 32-token
+// blocks).
 #define VPA_DECODE_FP8_DBS(T)                                  \
   if (D == 64 && BS == 16) { VPA_DECODE_FP8_G(T, 64, 16) }     \
   if (D == 64 && BS == 32) { VPA_DECODE_FP8_G(T, 64, 32) }     \
@@ -1383,15 +1443,18 @@ hipError_t launch_decode_f32_fp8(void* out, const void* q, const void* kc, const
   if (D == 96 && BS == 32) { VPA_DECODE_FP8_G(T, 96, 32) }     \
   if (D == 192 && BS == 16) { VPA_DECODE_FP8_G(T, 192, 16) }   \
   if (D == 256 && BS == 8) { VPA_DECODE_FP8_G(T, 256, 8) }     \
-  if (D == 256 && BS == 16) { VPA_DECODE_FP8_G(T, 256, 16) }
+  if (D == 256 && BS == 16) { VPA_DECODE_FP8_G(T, 256, 16) }   \
+  if (D == 192 && BS == 32) { VPA_DECODE_GENERIC_FP8_G(T, 192, 32) } \
+  if (D == 256 && BS == 32) { VPA_DECODE_GENERIC_FP8_G(T, 256, 32) }
 
 #define VPA_DECODE_F32_FP8_G(D, BS)                                       \
   if (group == 1) return launch_decode_f32_fp8<D, BS, 1>(args...);        \
   if (group == 2) return launch_decode_f32_fp8<D, BS, 2>(args...);        \
   if (group == 4) return launch_decode_f32_fp8<D, BS, 4>(args...);
 
-// fp8 caches: the rows kernel for bf16 / f16 queries; f32 queries on the
-// generic split-K kernel (decode_f32_fp8_shape).
+// fp8 caches: the rows kernel for bf16 / f16 queries (the generic split-K
+// kernel at head dims 192 and 256 with 32-token blocks); f32 queries on the
+// generic kernel (decode_f32_fp8_shape).
 template <typename... A>
 hipError_t dispatch_decode_fp8(int dtype, int D, int BS, int group, A... args) {
   if (dtype == VPA_DTYPE_BF16) { VPA_DECODE_FP8_DBS(bf16_t) }
@@ -1598,6 +1661,8 @@ bool decode_f32_fp8_shape(int head_dim, int block_size) {
 
 bool decode_fp8_shape(int head_dim, int block_size) {
   if (!cache_kernels_supported(VPA_DTYPE_FP8_E4M3, head_dim, block_size)) return false;
+  // the two 16-bit tiles the rows kernel does not take: the generic kernel
+  if (block_size == 32 && (head_dim == 192 || head_dim == 256)) return true;
   if (!decode_uses_rows_kernel(VPA_DTYPE_BF16, head_dim, block_size)) return false;
   // a whole number of 1 KiB loads per fp8 tile (at 8-token blocks a value
   // unit holds two dims: head dims 128 and 256)

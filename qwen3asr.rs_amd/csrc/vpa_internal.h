@@ -258,8 +258,9 @@ bool decode_supported(int dtype, int head_dim, int block_size, int group);
 // shapes with the generic split-K kernel. The work list depends on this
 // choice only, so it is the same for every cache type.
 bool decode_uses_rows_kernel(int dtype, int head_dim, int block_size);
-// fp8 caches decode on the rows kernel: head dims 64 and 128 at 16- and
-// 32-token blocks, 128 at 8, 96 at 32, 192 at 16, 256 at 8 and 16.
+// fp8 caches under 16-bit queries: on the rows kernel head dims 64 and 128
+// at 16- and 32-token blocks, 128 at 8, 96 at 32, 192 at 16, 256 at 8 and
+// 16; on the generic split-K kernel 192 and 256 at 32.
 bool decode_fp8_shape(int head_dim, int block_size);
 // fp8 caches under f32 queries decode on the generic split-K kernel: blocks
 // of 16 or 32 tokens with a whole number of 1 KiB wave loads per tile.

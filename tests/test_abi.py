@@ -358,10 +358,14 @@ def test_reshape_and_cache_fp8_accepts_every_float_input(dtype):
           hstride=128 * 8), _lib.VPA_ERR_UNSUPPORTED, "f32 queries"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bs=8, bstride=8 * 64 * 8, hstride=64 * 8),
      _lib.VPA_ERR_UNSUPPORTED, "(got 64, 8)"),
+    # head dims 192 and 256 at 32-token blocks under 16-bit queries: the
+    # generic kernel, validation passes up to the workspace check
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bs=32, bstride=8 * 256 * 32, hstride=256 * 32),
-     _lib.VPA_ERR_UNSUPPORTED, "(got 256, 32)"),
+     _lib.VPA_ERR_WORKSPACE, "workspace"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=192, bs=32, bstride=8 * 192 * 32, hstride=192 * 32),
-     _lib.VPA_ERR_UNSUPPORTED, "(got 192, 32)"),
+     _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=192, bs=8, bstride=8 * 192 * 8, hstride=192 * 8),
+     _lib.VPA_ERR_UNSUPPORTED, "(got 192, 8)"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=96, bs=16, bstride=8 * 96 * 16, hstride=96 * 16),
      _lib.VPA_ERR_UNSUPPORTED, "(got 96, 16)"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES), _lib.VPA_ERR_WORKSPACE, "workspace"),

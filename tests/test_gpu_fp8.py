@@ -208,19 +208,36 @@ def test_fp8_decode_head_dims_and_groups(device, d, h, kvh):
 FP8_EDGES = [1, 7, 511, 512, 513, 2047, 2048, 2049, 4097, 6145]
 
 
-@pytest.mark.parametrize("d,bs", [(96, 32), (192, 16), (256, 8), (256, 16)])
+@pytest.mark.parametrize("d,bs", [(96, 32), (192, 16), (256, 8), (256, 16), (192, 32),
+                                  (256, 32)])
 @pytest.mark.parametrize("code,scales,planned", [(orc.BF16, (1.0, 1.0), False),
                                                  (orc.F16, (0.37, 3.1), True)])
 def test_fp8_decode_head_dims_96_192_256(device, d, bs, code, scales, planned):
     """fp8 caches at head dims 96 (32-token blocks), 192 (16) and 256 (8 and
-    16; at 8 a value unit holds two dims of the block's 8 tokens), with and
-    without scales, planned and not, over the wave and chunk edges."""
+    16; at 8 a value unit holds two dims of the block's 8 tokens) on the rows
+    kernel, 192 and 256 at 32-token blocks on the generic split-K kernel,
+    with and without scales, planned and not, over the wave, chunk and
+    partition edges."""
     got, want = fp8_decode_case(device, code, 16, 8, d, bs, FP8_EDGES, seed=d + bs + code,
                                 scales=scales, planned=planned)
     assert_attention_close(got, want, code, f"fp8 d={d} bs={bs} code={code}")
 
 
-@pytest.mark.parametrize("d,bs", [(96, 32), (256, 16)])
+@pytest.mark.parametrize("d", [192, 256])
+@pytest.mark.parametrize("code,scales", [(orc.BF16, (0.6, 1.7)), (orc.BF16, (0.37, 3.1)),
+                                         (orc.F16, (1.9, 0.45))])
+def test_fp8_decode_generic_kernel_rounds_like_the_reference(device, d, code, scales):
+    """16-bit queries over fp8 caches at 32-token blocks (head dims 192 and
+    256, the generic split-K kernel): each element is dequantised as the
+    reference does, f32(E4M3FN(byte) * scale) rounded to the query type, so
+    non-unit scales stay within the element-wise bound against the fp64
+    oracle's same dequantisation (bf16 included)."""
+    got, want = fp8_decode_case(device, code, 16, 8, d, 32, FP8_EDGES, seed=d + 7 * code + 3,
+                                scales=scales, planned=False)
+    assert_attention_close(got, want, code, f"fp8 generic d={d} code={code} scales={scales}")
+
+
+@pytest.mark.parametrize("d,bs", [(96, 32), (256, 16), (256, 32)])
 @pytest.mark.parametrize("h,kvh", [(8, 8), (16, 4), (64, 8)])
 def test_fp8_decode_head_dims_groups(device, d, bs, h, kvh):
     got, want = fp8_decode_case(device, orc.BF16, h, kvh, d, bs, [3, 64, 300, 2500],
