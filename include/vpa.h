@@ -151,13 +151,18 @@ size_t vpa_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * Any number of query heads per kv head: the kernels serve 1, 2 or 4 per
  * kv head, and a larger G runs as G / 4 (or / 2, / 1 where 4 does not
  * divide G) replicas of each kv head, each reading that head's tiles.
- * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 with a bf16 or f16
- * query (head_dim 64 or 128 with block_size 16 or 32, 128 or 256 with 8,
- * 96 with 32, 192 or 256 with 16 or 32) or an f32 query (block_size 16 or 32,
- * tiles of at most 6 KiB: every head_dim but 96 at 16 tokens and 256 at 32):
- * K and V are then read as
- * (float)byte * (*k_scale) and (float)byte * (*v_scale), k_scale / v_scale
- * being device pointers to one f32 each (ignored for 16/32-bit caches).
+ * cache_dtype equals dtype, or is VPA_DTYPE_FP8_E4M3 under any query type:
+ * K and V are then read as (float)byte * (*k_scale) and
+ * (float)byte * (*v_scale), k_scale / v_scale being device pointers to one
+ * f32 each (ignored for 16/32-bit caches). Every head_dim of {64, 96, 128,
+ * 192, 256} and block_size of {8, 16, 32} is served: the decode kernels
+ * take the (block, head) tiles that are whole 1 KiB wave loads (fp8 under
+ * 16-bit queries: head_dim 64 or 128 with block_size 16 or 32, 128 or 256
+ * with 8, 96 with 32, 192 or 256 with 16 or 32; under f32 queries block_size
+ * 16 or 32 with tiles of at most 6 KiB), and the other pairs (16-bit
+ * head_dim 96 at block_size 8, the remaining fp8 ones) run on the
+ * chunked-prefill vector kernel with one query per sequence, at vector-ALU
+ * speed and with the same results contract.
  * workspace must hold vpa_paged_attention_workspace_size(...) bytes (always
  * non-zero for num_seqs > 0: it carries the per-call work list) and be
  * 256-byte aligned. Two calls that run concurrently need two workspaces.

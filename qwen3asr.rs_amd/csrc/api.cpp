@@ -273,16 +273,25 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
   if (rc != VPA_OK) return rc;
   rc = check_scales(op, cache_dtype, k_scale, v_scale);
   if (rc != VPA_OK) return rc;
-  if (fp8 && dtype != VPA_DTYPE_F32 && !decode_fp8_shape(head_dim, block_size))
+  // The decode kernels take the shapes whose (block, head) tiles are whole
+  // 1 KiB wave loads (decode_supported, decode_fp8_shape,
+  // decode_f32_fp8_shape); the other head-dim / block-size pairs of the
+  // reference's set (16-bit head dim 96 at 8-token blocks; fp8 caches at
+  // head dim 64 with 8, 96 with 8 or 16, 192 with 8; under f32 queries
+  // 8-token blocks and head dim 256 with 32) run on the chunked-prefill
+  // vector kernel, one query per sequence over its whole context, at
+  // vector-ALU speed.
+  const bool own_kernel =
+      fp8 ? (dtype == VPA_DTYPE_F32 ? decode_f32_fp8_shape(head_dim, block_size)
+                                    : decode_fp8_shape(head_dim, block_size))
+          : decode_supported(dtype, head_dim, block_size, 1);
+  const bool on_vector =
+      !own_kernel && prefill_vector_supported(dtype, cache_dtype, head_dim, block_size);
+  if (!own_kernel && !on_vector)
     return fail(VPA_ERR_UNSUPPORTED,
-                "%s: fp8 cache needs head_dim 64 or 128 with block_size 16 or 32, 128 or 256 "
-                "with 8, 96 with 32, 192 or 256 with 16 or 32 (got %d, %d)",
-                op, head_dim, block_size);
-  if (fp8 && dtype == VPA_DTYPE_F32 && !decode_f32_fp8_shape(head_dim, block_size))
-    return fail(VPA_ERR_UNSUPPORTED,
-                "%s: fp8 cache under f32 queries needs block_size 16 or 32 and a whole number "
-                "of 1 KiB wave loads per (block, head) tile (got head_dim %d, block_size %d)",
-                op, head_dim, block_size);
+                "%s: no decode kernel for %s queries over a %s cache at head_dim=%d "
+                "block_size=%d (head_dim 64/96/128/192/256, block_size 8/16/32)",
+                op, dtype_name(dtype), dtype_name(cache_dtype), head_dim, block_size);
   if (num_seqs < 0 || num_heads <= 0 || max_context_len < 0 || block_table_stride < 0)
     return fail(VPA_ERR_INVALID_ARGUMENT,
                 "%s: bad sizes num_seqs=%d num_heads=%d max_context_len=%d "
@@ -292,12 +301,6 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
     return fail(VPA_ERR_INVALID_ARGUMENT, "%s: num_heads=%d not a multiple of num_kv_heads=%d",
                 op, num_heads, num_kv_heads);
   const int group = num_heads / num_kv_heads;
-  if (!decode_supported(dtype, head_dim, block_size, group))
-    return fail(VPA_ERR_UNSUPPORTED,
-                "%s: no decode kernel for %s head_dim=%d block_size=%d (a (block, head) tile "
-                "must be a multiple of 1 KiB: head_dim 96 needs 16- or 32-token blocks at "
-                "16 bits)",
-                op, dtype_name(dtype), head_dim, block_size);
   if (max_context_len > kDecodeMaxPartitions * kDecodeMinPartitionTokens)
     return fail(VPA_ERR_UNSUPPORTED, "%s: max_context_len=%d exceeds %d", op, max_context_len,
                 kDecodeMaxPartitions * kDecodeMinPartitionTokens);
@@ -401,7 +404,16 @@ int paged_attention_impl(void* out, const void* query, const float* k_scale,
         last, num_seqs, g, k_scale, v_scale, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) rc_l = hip_status(op, e);
   }
-  if (rc_l == VPA_OK)
+  if (rc_l == VPA_OK && on_vector)
+    // one causal query per sequence (row s), the decode's 1e-6 in the
+    // denominator
+    rc_l = hip_status(op, launch_prefill_vector(
+                              dtype, cache_dtype, out, query, key_cache, value_cache,
+                              block_tables, block_table_stride, nullptr, context_lens, num_seqs,
+                              1, max_context_len, num_seqs, softmax_scale, 1e-6f, 1, num_heads,
+                              g, fp8 ? k_scale : nullptr, fp8 ? v_scale : nullptr,
+                              static_cast<hipStream_t>(stream)));
+  else if (rc_l == VPA_OK)
     rc_l = hip_status(op, launch_paged_decode(dtype, cache_dtype, out, query, key_cache,
                                             value_cache, block_tables, block_table_stride,
                                             context_lens, max_context_len, softmax_scale,
@@ -501,7 +513,10 @@ int vpa_paged_attention_plan(const uint32_t* context_lens, int32_t max_context_l
                 "block_size=%d max_context_len=%d block_table_stride=%d",
                 op, num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_context_len,
                 block_table_stride);
-  if (!decode_supported(dtype, head_dim, block_size, num_heads / num_kv_heads))
+  // (shapes the decode kernels do not take run on the chunked-prefill
+  // vector kernel, which needs no plan)
+  if (!decode_supported(dtype, head_dim, block_size, num_heads / num_kv_heads) &&
+      !prefill_vector_supported(dtype, dtype, head_dim, block_size))
     return fail(VPA_ERR_UNSUPPORTED, "%s: no decode kernel for this configuration", op);
   if (max_context_len > kDecodeMaxPartitions * kDecodeMinPartitionTokens)
     return fail(VPA_ERR_UNSUPPORTED, "%s: max_context_len=%d exceeds %d", op, max_context_len,

@@ -8,6 +8,10 @@
 // mod.rs:145-283), and the 16-bit head-dim / block-size pairs without a
 // whole number of 1 KiB DMAs per tile.
 //
+// Decode (paged_attention) runs the head-dim / block-size pairs its own
+// kernels do not take on this kernel too, with one query per sequence (no
+// cu_seqlens_q), causal, over the whole context, and denom_eps 1e-6.
+//
 // Semantics are the MFMA kernel's: query i of a sequence with n queries and
 // L keys sees keys t <= i + L - n when causal (bottom-right alignment, the
 // cached-causal mask of vasr-models/src/model/attention.rs:78-149), every key
@@ -118,7 +122,9 @@ __global__ __launch_bounds__(kVThreads) void prefill_paged_vector_kernel(
   const int s = rest / row_tiles;
   const int rt = rest % row_tiles;
 
-  const uint32_t qa = cu_seqlens_q[s], qb = cu_seqlens_q[s + 1];
+  // (no cu_seqlens_q: one query per sequence, row s — the decode form)
+  const uint32_t qa = cu_seqlens_q != nullptr ? cu_seqlens_q[s] : (uint32_t)s;
+  const uint32_t qb = cu_seqlens_q != nullptr ? cu_seqlens_q[s + 1] : (uint32_t)s + 1u;
   int q_len = qb > qa ? (int)min(qb - qa, (uint32_t)max_query_len) : 0;
   if ((int64_t)qa >= total_query_rows) q_len = 0;
   else q_len = (int)min((int64_t)q_len, total_query_rows - (int64_t)qa);

@@ -246,12 +246,14 @@ def test_prefill_head_dims_pass_validation(d, bs, fp8):
 
 
 @pytest.mark.parametrize("d,bs,dtype,ok", [
-    (96, 8, _lib.DTYPE_BF16, False), (96, 16, _lib.DTYPE_BF16, True),
+    (96, 8, _lib.DTYPE_BF16, True), (96, 16, _lib.DTYPE_BF16, True),
     (96, 8, _lib.DTYPE_F32, True), (192, 8, _lib.DTYPE_F16, True),
     (80, 16, _lib.DTYPE_BF16, False)])
 def test_decode_head_dims_validation(d, bs, dtype, ok):
-    """Decode at head_dim 96 and 192: a (block, head) tile must be whole 1 KiB
-    wave loads (16-bit head_dim 96 needs 16- or 32-token blocks)."""
+    """Decode at head_dim 96 and 192 passes validation at every block size
+    (16-bit head_dim 96 at 8-token blocks, whose tile is not whole 1 KiB wave
+    loads, on the chunked-prefill vector kernel); head_dim 80 is outside the
+    reference's set."""
     rc, msg = pa_call(d=d, bs=bs, dtype=dtype, cdtype=dtype, bstride=8 * d * bs,
                       hstride=d * bs, b=0)
     if ok:
@@ -352,22 +354,26 @@ def test_reshape_and_cache_fp8_accepts_every_float_input(dtype):
      _lib.VPA_ERR_WORKSPACE, "workspace"),
     (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, d=192, bs=32,
           bstride=8 * 192 * 32, hstride=192 * 32), _lib.VPA_ERR_WORKSPACE, "workspace"),
+    # the pairs no decode kernel takes run on the chunked-prefill vector
+    # kernel: validation passes up to the workspace check
     (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bs=32,
-          bstride=8 * 256 * 32, hstride=256 * 32), _lib.VPA_ERR_UNSUPPORTED, "f32 queries"),
+          bstride=8 * 256 * 32, hstride=256 * 32), _lib.VPA_ERR_WORKSPACE, "workspace"),
     (dict(dtype=_lib.DTYPE_F32, cdtype=FP8, ks=FAKE, vs=FAKE, bs=8, bts=128, bstride=8 * 128 * 8,
-          hstride=128 * 8), _lib.VPA_ERR_UNSUPPORTED, "f32 queries"),
-    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bs=8, bstride=8 * 64 * 8, hstride=64 * 8),
-     _lib.VPA_ERR_UNSUPPORTED, "(got 64, 8)"),
+          hstride=128 * 8), _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=64, bs=8, bts=128, bstride=8 * 64 * 8,
+          hstride=64 * 8), _lib.VPA_ERR_WORKSPACE, "workspace"),
     # head dims 192 and 256 at 32-token blocks under 16-bit queries: the
     # generic kernel, validation passes up to the workspace check
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=256, bs=32, bstride=8 * 256 * 32, hstride=256 * 32),
      _lib.VPA_ERR_WORKSPACE, "workspace"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=192, bs=32, bstride=8 * 192 * 32, hstride=192 * 32),
      _lib.VPA_ERR_WORKSPACE, "workspace"),
-    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=192, bs=8, bstride=8 * 192 * 8, hstride=192 * 8),
-     _lib.VPA_ERR_UNSUPPORTED, "(got 192, 8)"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=192, bs=8, bts=128, bstride=8 * 192 * 8,
+          hstride=192 * 8), _lib.VPA_ERR_WORKSPACE, "workspace"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=96, bs=16, bstride=8 * 96 * 16, hstride=96 * 16),
-     _lib.VPA_ERR_UNSUPPORTED, "(got 96, 16)"),
+     _lib.VPA_ERR_WORKSPACE, "workspace"),
+    (dict(cdtype=FP8, ks=FAKE, vs=FAKE, d=80, bs=16, bstride=8 * 80 * 16, hstride=80 * 16),
+     _lib.VPA_ERR_UNSUPPORTED, "no kernel"),
     (dict(cdtype=FP8, ks=FAKE, vs=FAKE, **F8_STRIDES), _lib.VPA_ERR_WORKSPACE, "workspace"),
     # head dims 96 / 192 / 256 on the rows kernel: validation passes up to
     # the workspace check
