@@ -1,13 +1,19 @@
-// Paged-attention decode for gfx950, two paths:
-//   * 16-bit and fp8 caches with head_dim 64 or 128 (vASR's shapes): a work
-//     list built on the device (decode_plan_kernel, longest chunk first),
-//     paged_decode_rows_kernel (one workgroup per (chunk, kv head), its
-//     waves splitting the chunk's blocks) and decode_merge_kernel for the
-//     sequences longer than one chunk; described further down;
-//   * f32 caches and head_dim 96, 192, 256: paged_decode_kernel, one wavefront per
-//     (kv head, sequence, split-K partition of kDecodePartitionTokens
-//     tokens) serving all the query heads of that kv head (GQA), and
-//     paged_decode_reduce_kernel merging the partitions; described here.
+// Paged-attention decode for gfx950, two paths here:
+//   * 16-bit and fp8 caches (under 16-bit queries) whose (block, head)
+//     tiles are whole 1 KiB wave loads of at most 8 KiB, vASR's shapes among
+//     them: a work list built on the device (decode_plan_kernel, longest
+//     chunk first), paged_decode_rows_kernel (one workgroup per (chunk, kv
+//     head), its waves splitting the chunk's blocks) and decode_merge_kernel
+//     for the sequences longer than one chunk; described further down;
+//   * f32 caches, fp8 caches under f32 queries, and the 16-bit / fp8 tiles
+//     above 8 KiB (head dims 192 and 256 at 32-token blocks):
+//     paged_decode_kernel, one wavefront per (kv head, sequence, split-K
+//     partition of kDecodePartitionTokens tokens) serving all the query
+//     heads of that kv head (GQA), and paged_decode_reduce_kernel merging
+//     the partitions; described here.
+// The head-dim / block-size pairs whose tiles are not whole 1 KiB loads run
+// on the chunked-prefill vector kernel (prefill_vector_kernels.hip) with one
+// query per sequence; api.cpp routes them.
 //
 // Semantics follow the reference's decode call
 // (vasr-models/src/model/thinker_text.rs:1126-1139) with the eager attention

@@ -187,7 +187,9 @@ hipError_t launch_prefill_paged(int dtype, int cache_dtype, void* out, const voi
 
 // The vector-ALU prefill (prefill_vector_kernels.hip): f32 queries over f32
 // or fp8 caches, any number of query heads per kv head, and the 16-bit
-// shapes the MFMA kernel does not take. Same arguments as launch_prefill_paged.
+// shapes the MFMA kernel does not take; also the decode of the head-dim /
+// block-size pairs no decode kernel takes (cu_seqlens_q null: one query per
+// sequence). Same arguments as launch_prefill_paged.
 bool prefill_vector_supported(int dtype, int cache_dtype, int head_dim, int block_size);
 int64_t prefill_vector_workgroups(int32_t num_seqs, int32_t max_query_len, int32_t group,
                                   int32_t num_kv_heads);
