@@ -18,7 +18,8 @@ import torch
 
 import vpa
 from oracle import oracle as orc
-from tests._util import assert_attention_close, make_cache, random_words, to_dev, to_host, u32
+from tests._util import (assert_attention_close, assert_attention_close_normwise, make_cache,
+                         random_words, to_dev, to_host, u32)
 from tests.test_gpu_decode import decode_case
 from tests.test_gpu_fp8 import fp8_decode_case
 from tests.test_gpu_fused_append import case as fused_case
@@ -108,3 +109,49 @@ def test_fused_append_on_vector_shapes_equals_two_calls(device, code, d, bs, fp8
     got = fused(device, c, code, max_ctx, d ** -0.5)
     for g, w, name in zip(got, want, ("out", "key_cache", "value_cache")):
         assert np.array_equal(g, w), f"{name} differs from the two calls"
+
+
+# (query type, head dim, block size) of every decode pair served outside the
+# rows kernel's fp8 / 16-bit instances: the vector kernel's pairs and the
+# generic kernel's fp8 tiles under 16-bit queries
+_FALLBACK = ([(c, 96, 8, False) for c in (orc.BF16, orc.F16)] +
+             [(c, d, bs, True) for c in (orc.BF16, orc.F16)
+              for d, bs in FP8_SHAPES_16 + [(192, 32), (256, 32)]] +
+             [(orc.F32, d, bs, True) for d, bs in [(64, 8), (96, 8), (128, 8), (192, 8),
+                                                   (256, 8), (256, 32)]])
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_decode_fallback_random(device, case):
+    """Seeded random draws over those pairs: query heads per kv head 1-8 (3
+    and 6 included), 1-8 sequences with lengths up to 3000 and block edges,
+    logit scales 0.5-1.5 of 1/sqrt(d), fp8 scales 0.3-1.5 and 0.2-3.0, against
+    the fp64 oracle: element-wise for 16-bit queries (these paths round each
+    dequantised fp8 element to the query type as the reference and the
+    oracle do); normwise for f32 queries over fp8 caches, where outputs near
+    zero are the residue of f32 sums over thousands of cancelling terms
+    (seed 31005: head dim 256, k_scale 1.5, 1.8x the element-wise bound at
+    about 1e-6 of the largest output)."""
+    rng = np.random.default_rng(31000 + case)
+    code, d, bs, fp8 = _FALLBACK[int(rng.integers(0, len(_FALLBACK)))]
+    g = int(rng.choice([1, 2, 3, 4, 6, 8]))
+    kvh = int(rng.choice([1, 2, 4, 8]))
+    n = int(rng.integers(1, 9))
+    lens = [int(v) for v in rng.integers(1, 3000, size=n)]
+    k = int(rng.integers(0, n + 1))
+    lens[:k] = [int(v) for v in rng.choice([1, bs - 1, bs, bs + 1, 31, 32, 33, 512, 2049], size=k)]
+    lens = [max(1, v) for v in lens]
+    scale = float(rng.uniform(0.5, 1.5)) * d ** -0.5
+    what = f"case {case}: code={code} d={d} bs={bs} fp8={fp8} h={g * kvh} kvh={kvh} lens={lens}"
+    if fp8:
+        scales = (float(rng.uniform(0.3, 1.5)), float(rng.uniform(0.2, 3.0)))
+        got, want = fp8_decode_case(device, code, g * kvh, kvh, d, bs, lens, seed=32000 + case,
+                                    scales=scales, softmax_scale=scale)
+        what += f" scales={scales}"
+    else:
+        got, want = decode_case(device, code, g * kvh, kvh, d, bs, lens, seed=32000 + case,
+                                scale=scale)
+    if fp8 and code == orc.F32:
+        assert_attention_close_normwise(got, want, code, what)
+    else:
+        assert_attention_close(got, want, code, what)
