@@ -451,13 +451,12 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Fast decode path for 16-bit caches with head_dim <= 128 (x = 8, at most 16
-// chunks per key row).
+// Fast decode path (16-bit caches, and fp8 caches under 16-bit queries,
+// whose (block, head) tiles are whole 1 KiB wave loads of at most 8 KiB).
 //
 // Work list: decode_plan_kernel (one workgroup) turns context_lens into the
 // list of (sequence, chunk) items, longest first, a chunk being NW * PT
-// tokens, plus the list of sequences that span several chunks and a small
-// header {0, item count, multi count}. All of it lives in the caller's
+// tokens, and a small header {0, item count}. All of it lives in the caller's
 // workspace and is rebuilt by every call, so the launches can be captured
 // in a graph and replayed with new lengths; max_context_len only sizes the
 // grid, surplus workgroups exit at once.
@@ -480,8 +479,10 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
 // The NW partial results are merged in LDS. A sequence of a single chunk
 // writes its output directly; a longer one writes one f32 partial row per
 // chunk (D values + a 32-float line holding {max (log2 units), sum}, whole
-// 128-byte lines), merged by decode_merge_kernel over the plan's list of multi-chunk
-// sequences. (Merging in the last workgroup to finish would need an
+// 128-byte lines), merged by decode_merge_kernel, whose waves read each
+// (sequence, head)'s length and skip the single-chunk ones (a list of the
+// multi-chunk sequences would put one more dependent load in front of the
+// partial rows of this latency-bound launch). (Merging in the last workgroup to finish would need an
 // agent-scope release per chunk, which on gfx950 writes back the XCD's L2:
 // measured with only that fence added, c3 decode went from 176 to 823 us
 // per layer, against 4.7 us for the extra launch.)
@@ -511,12 +512,10 @@ __device__ __forceinline__ int plan_bucket(int L, int p, int part_tokens) {
 __global__ __launch_bounds__(1024) void decode_plan_kernel(
     const uint32_t* __restrict__ context_lens, int32_t num_seqs, int32_t max_ctx,
     int32_t cap_tokens, int32_t part_tokens, uint2* __restrict__ items,
-    uint32_t* __restrict__ multi, uint32_t* __restrict__ queue) {
+    uint32_t* __restrict__ queue) {
   constexpr int NB = kPlanBuckets;
   __shared__ uint32_t s_wave[16][NB];
   __shared__ uint32_t s_base[NB + 1];
-  __shared__ uint32_t s_multi;
-  if (threadIdx.x == 0) s_multi = 0;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int per = (num_seqs + 1023) / 1024;
@@ -575,13 +574,10 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(
         if (c == b) at = pos[c]++;
       items[at] = make_uint2(((uint32_t)s << 16) | (uint32_t)p, (uint32_t)max(L, 0));
     }
-    if (n > 1) multi[atomicAdd(&s_multi, 1u)] = (uint32_t)s;
   }
-  __syncthreads();
   if (tid == 0) {
     queue[0] = 0u;
     queue[1] = s_base[NB];
-    queue[2] = s_multi;
   }
 }
 
@@ -1257,7 +1253,7 @@ hipError_t launch_decode_rows_c(void* out, const void* q, const void* kc, const 
   hipError_t e = hipSuccess;
   if (!ws.planned) {
     hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, cl, num_seqs,
-                       max_ctx, cap_tokens, kChunk, ws.items, ws.multi, ws.queue);
+                       max_ctx, cap_tokens, kChunk, ws.items, ws.queue);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1617,7 +1613,7 @@ hipError_t launch_decode_plan(int dtype, const uint32_t* context_lens, int32_t m
   if (!rows || num_seqs == 0) return hipSuccess;
   hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, context_lens, num_seqs,
                      max_context_len, block_table_stride * g.block_size, kDecodeChunk, ws.items,
-                     ws.multi, ws.queue);
+                     ws.queue);
   return hipGetLastError();
 }
 
@@ -1677,7 +1673,7 @@ bool decode_fp8_shape(int head_dim, int block_size) {
 
 namespace {
 struct WorkspacePlan {
-  size_t part_out, part_stat, items, multi, queue, total;
+  size_t part_out, part_stat, items, queue, total;
   int max_parts;
 };
 // Pieces of the decode scratch for split-K partitions of part_tokens tokens
@@ -1693,9 +1689,8 @@ WorkspacePlan plan_workspace(int num_seqs, int num_heads, int head_dim, int max_
   w.part_out = up(rows * (size_t)(head_dim + 32) * sizeof(float));
   w.part_stat = up(rows * sizeof(float));
   w.items = up((size_t)num_seqs * (size_t)(w.max_parts > 1 ? w.max_parts : 1) * sizeof(uint2));
-  w.multi = up((size_t)num_seqs * sizeof(uint32_t));
   w.queue = 256;
-  w.total = w.part_out + 2 * w.part_stat + w.items + w.multi + w.queue;
+  w.total = w.part_out + 2 * w.part_stat + w.items + w.queue;
   return w;
 }
 }  // namespace
@@ -1727,8 +1722,6 @@ DecodeWorkspace carve_decode_workspace(void* base, int num_seqs, int num_heads, 
   p += w.part_stat;
   ws.items = reinterpret_cast<uint2*>(p);
   p += w.items;
-  ws.multi = reinterpret_cast<uint32_t*>(p);
-  p += w.multi;
   ws.queue = reinterpret_cast<uint32_t*>(p);
   return ws;
 }

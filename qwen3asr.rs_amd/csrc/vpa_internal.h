@@ -43,8 +43,7 @@ struct DecodeWorkspace {
   float* part_max;   // [num_seqs, num_heads, max_parts]
   float* part_sum;   // [num_seqs, num_heads, max_parts]
   uint2* items;      // [num_seqs * max(1, max_parts)] work list {seq << 16 | partition, length}
-  uint32_t* multi;   // [num_seqs] sequences with more than one partition
-  uint32_t* queue;   // [3]: next work unit, number of items, number of multi entries
+  uint32_t* queue;   // [2]: next work unit, number of items
   int max_parts;     // ceil(max_context_len / partition tokens of the layout)
   bool planned = false;  // the work list is already in the workspace (skip the plan launch)
 };
