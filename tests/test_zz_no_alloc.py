@@ -6,9 +6,10 @@ the scratch layout differs), on two calls in a row, the second with a
 smaller batch and shorter contexts so that it runs over what the first left
 in the array. The second call is also checked against the fp64 oracle.
 Covered: the rows kernel with multi-chunk sequences (bf16, merge launch),
-the fp8-cache rows kernel, and the generic kernel (f32, 256-token
-partitions); calls on two streams; the call captured in a HIP graph and
-replayed. The rejection of a call larger than the scratch happens on the
+the fp8-cache rows kernel, the generic kernel (f32, 256-token partitions;
+fp8 tiles under bf16 queries at head dim 256 with 32-token blocks), a pair
+on the chunked-prefill vector kernel (head dim 96, 8-token blocks); calls
+on two streams; the call captured in a HIP graph and replayed. The rejection of a call larger than the scratch happens on the
 host before any device access and is tested in the CPU suite
 (tests/test_abi.py), where no GPU exists for a wrong launch to reach."""
 
@@ -26,7 +27,7 @@ pytestmark = pytest.mark.gpu
 H, KVH, D, BS = 16, 8, 128, 16
 
 
-def case(rng, code, lens, cache_code=None):
+def case(rng, code, lens, cache_code=None, D=D, BS=BS):
     cache_code = code if cache_code is None else cache_code
     nb = sum((int(L) + BS - 1) // BS for L in lens) + 8
     if cache_code == orc.FP8 and code == orc.F32:
@@ -45,7 +46,7 @@ def case(rng, code, lens, cache_code=None):
         kc, vc = make_cache(rng, nb, KVH, D, BS, cache_code)
     bt = block_tables_for(rng, lens, nb, BS)
     q = random_words(rng, (len(lens), H, D), code)
-    return dict(q=q, kc=kc, vc=vc, bt=bt, lens=np.asarray(lens, dtype=np.uint32), nb=nb)
+    return dict(q=q, kc=kc, vc=vc, bt=bt, lens=np.asarray(lens, dtype=np.uint32), nb=nb, D=D, BS=BS)
 
 
 def dev_cache(a, cache_code, device):
@@ -66,6 +67,7 @@ def call(device, c, code, cache_code, noalloc, max_ctx):
     one = torch.ones(1, dtype=torch.float32, device=device)
     ks = one.data_ptr() if cache_code == orc.FP8 else None
     b = len(c["lens"])
+    D, BS = c["D"], c["BS"]
     stride_b, stride_h = kc.stride(0), kc.stride(1)
     stream = torch.cuda.current_stream(device).cuda_stream
     common = (out.data_ptr(), q.data_ptr(), ks, ks, kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
@@ -83,22 +85,26 @@ def call(device, c, code, cache_code, noalloc, max_ctx):
     return to_host(out)
 
 
-@pytest.mark.parametrize("code,cache_code", [(orc.BF16, orc.BF16), (orc.BF16, orc.FP8),
-                                             (orc.F32, orc.F32), (orc.F32, orc.FP8)])
-def test_noalloc_equals_workspace_entry_point_twice(device, code, cache_code):
-    rng = np.random.default_rng(31 + code + 7 * cache_code)
+@pytest.mark.parametrize("code,cache_code,d,bs", [
+    (orc.BF16, orc.BF16, D, BS), (orc.BF16, orc.FP8, D, BS), (orc.F32, orc.F32, D, BS),
+    (orc.F32, orc.FP8, D, BS),
+    # the generic split-K kernel over fp8 tiles under 16-bit queries, and a
+    # pair on the chunked-prefill vector kernel (no scratch used)
+    (orc.BF16, orc.FP8, 256, 32), (orc.BF16, orc.BF16, 96, 8)])
+def test_noalloc_equals_workspace_entry_point_twice(device, code, cache_code, d, bs):
+    rng = np.random.default_rng(31 + code + 7 * cache_code + d + bs)
     first = [int(x) for x in rng.integers(1, 4500, size=40)]
     first[:4] = [4096, 2049, 2048, 1]  # multi-chunk and single-chunk rows
     second = [int(x) for x in rng.integers(1, 1500, size=17)]
     for lens in (first, second):
-        c = case(rng, code, lens, cache_code)
+        c = case(rng, code, lens, cache_code, d, bs)
         max_ctx = int(max(lens))
         got = call(device, c, code, cache_code, True, max_ctx)
         want = call(device, c, code, cache_code, False, max_ctx)
         assert np.array_equal(got, want), f"batch {len(lens)}: noalloc differs from workspace call"
         assert np.all(np.isfinite(orc.to_f32(got, code)))
     # the second (smaller) call against the oracle
-    ref = orc.paged_attention(c["q"], c["kc"], c["vc"], c["bt"], c["lens"], max_ctx, D ** -0.5,
+    ref = orc.paged_attention(c["q"], c["kc"], c["vc"], c["bt"], c["lens"], max_ctx, d ** -0.5,
                               dtype=code, kv_dtype=orc.FP8 if cache_code == orc.FP8 else None)
     assert_attention_close(orc.to_f32(got, code), ref, code, "noalloc second call")
 
