@@ -126,7 +126,7 @@ def test_decode_config_c3_layer(device):
     16, 4096), the layer's own shuffled pool of ~1.1 GB): the decode append
     of 256 tokens is bit-exact over the whole pool (every other byte
     unchanged), and attention over all 256 sequences matches the oracle on
-    a sample that includes the longest sequence and multi-chunk ones."""
+    every sequence and head."""
     from vpa import workloads
     w = workloads.c3(num_layers=1)
     layer = w.layers[0]
@@ -150,14 +150,11 @@ def test_decode_config_c3_layer(device):
     assert np.array_equal(to_host(kc_d), kc)
     assert np.array_equal(to_host(vc_d), vc)
     lens = w.context_lens
-    sample = sorted({int(np.argmax(lens)), int(np.argmin(lens)),
-                     *np.nonzero(lens > 2048)[0][:4].tolist(),
-                     *np.nonzero((lens > 512) & (lens <= 1024))[0][:3].tolist(), 0, 1, 255})
-    q = to_host(q_d)[sample]
-    want = orc.paged_attention(q, kc, vc, layer.block_tables[sample], lens[sample],
+    want = orc.paged_attention(to_host(q_d), kc, vc, layer.block_tables, lens,
                                w.max_context_len, 128 ** -0.5, dtype=code)
-    got = orc.to_f32(to_host(out), code)[sample]
-    assert_attention_close(got, want, code, f"c3 sample {sample}")
+    got = orc.to_f32(to_host(out), code)
+    for s in range(len(lens)):
+        assert_attention_close(got[s], want[s], code, f"c3 seq {s} (context {int(lens[s])})")
 
 
 # lengths at the rows kernel's per-wave (512-token) and per-chunk
