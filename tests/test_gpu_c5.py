@@ -83,7 +83,7 @@ def test_c5_full_pool_append_and_decode(device):
             # attention on a sample of sequences against the oracle
             lens = w.context_lens
             pick = np.unique(np.concatenate([[int(lens.argmin()), int(lens.argmax())],
-                                             rng.choice(w.num_seqs, size=22, replace=False)]))
+                                             rng.choice(w.num_seqs, size=126, replace=False)]))
             blocks, tables, _ = workloads.compact_tables(layer.block_tables[pick], lens[pick], bs)
             idx = torch.from_numpy(blocks).to(device)
             kh, vh = to_host(kc.index_select(0, idx)), to_host(vc.index_select(0, idx))
