@@ -9,7 +9,7 @@ unplanned call, layer 1 through plan + planned call). Checks:
 * appends bit-exact: every slot written by exactly one sequence holds that
   sequence's new K and V rows (sequences may share blocks in c5, so a slot
   two sequences write is left out);
-* attention: the shortest and the longest sequence and 22 random ones
+* attention: the shortest and the longest sequence and 126 random ones
   against the fp64 oracle over their blocks copied to host memory
   (workloads.compact_tables), bf16 tolerance 2e-2;
 * every output row finite."""
