@@ -9,8 +9,8 @@ unplanned call, layer 1 through plan + planned call). Checks:
 * appends bit-exact: every slot written by exactly one sequence holds that
   sequence's new K and V rows (sequences may share blocks in c5, so a slot
   two sequences write is left out);
-* attention: the shortest and the longest sequence and 126 random ones
-  against the fp64 oracle over their blocks copied to host memory
+* attention: every sequence against the fp64 oracle over its blocks
+  copied to host memory
   (workloads.compact_tables), bf16 tolerance 2e-2;
 * every output row finite."""
 
@@ -47,7 +47,6 @@ def test_c5_full_pool_append_and_decode(device):
         vc = torch.randn((nb, kvh, d, bs), generator=g, device=device, dtype=bf)
         ctx = torch.from_numpy(w.context_lens).to(device)
         ws = vpa.paged_attention_workspace(w.num_seqs, h, d, w.max_context_len, device)
-        rng = np.random.default_rng(55)
         scale = d ** -0.5
         for li, layer in enumerate(w.layers):
             print(f"c5 layer {li}: append + {'planned' if li else 'unplanned'} decode",
@@ -80,10 +79,10 @@ def test_c5_full_pool_append_and_decode(device):
             assert torch.equal(got_v.view(torch.int16), v[once].view(torch.int16)), "V append"
             assert bool(torch.isfinite(out).all()), "non-finite attention output"
 
-            # attention on a sample of sequences against the oracle
+            # attention on every sequence against the oracle (their blocks,
+            # about 17 GB, copied out to host memory)
             lens = w.context_lens
-            pick = np.unique(np.concatenate([[int(lens.argmin()), int(lens.argmax())],
-                                             rng.choice(w.num_seqs, size=126, replace=False)]))
+            pick = np.arange(w.num_seqs)
             blocks, tables, _ = workloads.compact_tables(layer.block_tables[pick], lens[pick], bs)
             idx = torch.from_numpy(blocks).to(device)
             kh, vh = to_host(kc.index_select(0, idx)), to_host(vc.index_select(0, idx))
