@@ -9,8 +9,9 @@ denominator. Checked against the fp64 oracle of the decode
 (attention.rs:243-286 semantics; fp8 elements f32(E4M3FN(byte) * scale)
 rounded to the query type, as the reference dequantises) over the edges of
 the 32-key tiles and of the blocks, empty contexts, stale NaN past every
-context, scales, 1 to 8 query heads per kv head, the planned form, and the
-fused append entry point against its two calls."""
+context, scales, 1 to 8 query heads per kv head, the planned form, padded
+table columns, graph replays against eager calls, and the fused append
+entry point against its two calls."""
 
 import numpy as np
 import pytest
@@ -18,8 +19,8 @@ import torch
 
 import vpa
 from oracle import oracle as orc
-from tests._util import (assert_attention_close, assert_attention_close_normwise, make_cache,
-                         random_words, to_dev, to_host, u32)
+from tests._util import (assert_attention_close, assert_attention_close_normwise,
+                         block_tables_for, make_cache, random_words, to_dev, to_host, u32)
 from tests.test_gpu_decode import decode_case
 from tests.test_gpu_fp8 import fp8_decode_case
 from tests.test_gpu_fused_append import case as fused_case
@@ -155,3 +156,52 @@ def test_decode_fallback_random(device, case):
         assert_attention_close_normwise(got, want, code, what)
     else:
         assert_attention_close(got, want, code, what)
+
+
+def test_decode_vector_pair_padded_columns_and_larger_max_context(device):
+    """max_context_len above every context and padded block-table columns
+    (the graph-padding case) leave the result unchanged."""
+    lens = [1, 9, 100, 1000]
+    a, want = decode_case(device, orc.BF16, 16, 8, 96, 8, lens, seed=61)
+    b, _ = decode_case(device, orc.BF16, 16, 8, 96, 8, lens, seed=61, pad_cols=40,
+                       max_ctx=1000 + 40 * 8)
+    assert np.array_equal(a, b)
+    assert_attention_close(a, want, orc.BF16, "d=96 bs=8 padded")
+
+
+def test_decode_vector_pair_graph_replays_match_eager(device):
+    """paged_attention at a vector-kernel pair captured in a HIP graph and
+    replayed with new queries and longer contexts copied into the captured
+    buffers: every replay equals the eager call bit for bit."""
+    rng = np.random.default_rng(71)
+    code, d, bs, h, kvh = orc.BF16, 96, 8, 16, 8
+    lens0 = np.array([5, 40, 333, 900], dtype=np.uint32)
+    max_ctx = 1024
+    nb = len(lens0) * (max_ctx // bs) + 8
+    kc, vc = make_cache(rng, nb, kvh, d, bs, code)
+    bt = block_tables_for(rng, [max_ctx] * len(lens0), nb, bs)
+    kc_d, vc_d, bt_d = to_dev(kc, code, device), to_dev(vc, code, device), u32(bt, device)
+    q_d = to_dev(random_words(rng, (len(lens0), h, d), code), code, device)
+    ctx = u32(lens0, device)
+    ws = vpa.paged_attention_workspace(len(lens0), h, d, max_ctx, device)
+    out = torch.empty_like(q_d)
+
+    def call(o):
+        vpa.paged_attention(q_d, None, None, kc_d, vc_d, bt_d, ctx, None, max_ctx, d ** -0.5,
+                            1.0, None, out=o, workspace=ws)
+
+    call(out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(out)
+    torch.cuda.synchronize()
+    for t in range(1, 5):
+        q_d.copy_(to_dev(random_words(rng, (len(lens0), h, d), code), code, device))
+        ctx.copy_(u32(np.minimum(lens0 + 50 * t, max_ctx), device))
+        want = torch.empty_like(out)
+        call(want)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {t}"
