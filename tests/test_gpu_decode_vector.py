@@ -169,25 +169,39 @@ def test_decode_vector_pair_padded_columns_and_larger_max_context(device):
     assert_attention_close(a, want, orc.BF16, "d=96 bs=8 padded")
 
 
-def test_decode_vector_pair_graph_replays_match_eager(device):
-    """paged_attention at a vector-kernel pair captured in a HIP graph and
-    replayed with new queries and longer contexts copied into the captured
-    buffers: every replay equals the eager call bit for bit."""
-    rng = np.random.default_rng(71)
-    code, d, bs, h, kvh = orc.BF16, 96, 8, 16, 8
+@pytest.mark.parametrize("d,bs,fp8", [(96, 8, False), (256, 32, True)])
+def test_decode_graph_replays_match_eager(device, d, bs, fp8):
+    """paged_attention at a vector-kernel pair (head dim 96, 8-token blocks)
+    and on the generic kernel's fp8 tiles (head dim 256, 32-token blocks,
+    bf16 queries) captured in a HIP graph and replayed with new queries and
+    longer contexts copied into the captured buffers (lengths crossing the
+    generic kernel's partitions): every replay equals the eager call bit for
+    bit."""
+    rng = np.random.default_rng(71 + d)
+    code, h, kvh = orc.BF16, 16, 8
     lens0 = np.array([5, 40, 333, 900], dtype=np.uint32)
     max_ctx = 1024
     nb = len(lens0) * (max_ctx // bs) + 8
-    kc, vc = make_cache(rng, nb, kvh, d, bs, code)
-    bt = block_tables_for(rng, [max_ctx] * len(lens0), nb, bs)
-    kc_d, vc_d, bt_d = to_dev(kc, code, device), to_dev(vc, code, device), u32(bt, device)
+    if fp8:
+        kc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d // 16, bs, 16)) * 2)
+                              .astype(np.float32))
+        vc = orc.fp8_from_f32((rng.standard_normal((nb, kvh, d, bs)) * 2).astype(np.float32))
+        kc_d = torch.from_numpy(kc).to(device).view(torch.float8_e4m3fn)
+        vc_d = torch.from_numpy(vc).to(device).view(torch.float8_e4m3fn)
+        ks = torch.tensor([0.8], dtype=torch.float32, device=device)
+        vs = torch.tensor([1.3], dtype=torch.float32, device=device)
+    else:
+        kc, vc = make_cache(rng, nb, kvh, d, bs, code)
+        kc_d, vc_d = to_dev(kc, code, device), to_dev(vc, code, device)
+        ks = vs = None
+    bt_d = u32(block_tables_for(rng, [max_ctx] * len(lens0), nb, bs), device)
     q_d = to_dev(random_words(rng, (len(lens0), h, d), code), code, device)
     ctx = u32(lens0, device)
     ws = vpa.paged_attention_workspace(len(lens0), h, d, max_ctx, device)
     out = torch.empty_like(q_d)
 
     def call(o):
-        vpa.paged_attention(q_d, None, None, kc_d, vc_d, bt_d, ctx, None, max_ctx, d ** -0.5,
+        vpa.paged_attention(q_d, ks, vs, kc_d, vc_d, bt_d, ctx, None, max_ctx, d ** -0.5,
                             1.0, None, out=o, workspace=ws)
 
     call(out)
